@@ -1,0 +1,215 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput on one MI355X: Mixtral-8x7B-shape layer, prefill batch.
+
+Workload: hidden 4096, 8 experts, top-2 (softmax, renormalised), SwiGLU
+intermediate 14336, bf16 weights N(0,0.02), activations N(0,1), router logits
+x @ gate_w with gate_w N(0,0.02); 8192 tokens (default).  One step = one full
+layer forward (router -> align -> gate/up+SiLU -> down -> combine) through the
+single C-ABI entry point, inputs resident in HBM.
+
+Prints ONE JSON line.  Besides the contract fields it carries:
+  roofline      the dominant kernel (grouped gate/up GEMM + SiLU): algorithmic
+                FLOPs per launch / its mean duration from HIP events on the
+                launch stream, against the bf16 dense MFMA peak
+  cpu_baseline  the CPU oracle (fp32 PyTorch restatement of the layer) on a
+                bounded token sample, timed on this host
+  layer / decode / kernels_ms   whole-layer TFLOP/s, the 64-token decode batch
+                (HBM-bound) and the per-kernel breakdown
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+FP8_PEAK_TFLOPS = 5000.0
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+METRIC = "MoE-layer tokens/s + TFLOP/s (% MFMA peak) on 1 MI355X; vs host-CPU ref"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=8192)
+    ap.add_argument("--decode-tokens", type=int, default=64)
+    ap.add_argument("--cpu-tokens", type=int, default=1024, help="token sample for the CPU baseline (0 = skip)")
+    ap.add_argument("--cpu-runs", type=int, default=3)
+    return ap.parse_args()
+
+
+def timed(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def stage_times(inp, steps, warmup, torch, ops):
+    """Same kernels as the fused entry point, launched one by one with HIP events
+    between them on the launch stream; returns mean ms per stage."""
+    s = inp.shape
+    T, H = inp.x.shape
+    n_local = inp.w_gate_up.shape[0]
+    A = T * s.top_k
+    names = ["router", "align", "gate_up_silu", "down", "combine"]
+    sums = [0.0] * len(names)
+
+    def once(evs):
+        evs[0].record()
+        ids, w = ops.router_topk(inp.logits, s.top_k, s.renormalize)
+        evs[1].record()
+        al = ops.align(ids, n_local, 0)
+        evs[2].record()
+        h = ops.gemm_gate_up_silu(inp.x, inp.w_gate_up, al["offsets"], A, a_rows=al["sorted_tok"])
+        evs[3].record()
+        y = ops.gemm_down(h, inp.w_down, al["offsets"], A, out_dtype=torch.bfloat16)
+        evs[4].record()
+        ops.combine(y, al["pos"], w, out_dtype=torch.bfloat16)
+        evs[5].record()
+
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+    for _ in range(warmup):
+        once(evs)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        once(evs)
+        torch.cuda.synchronize()
+        for i in range(len(names)):
+            sums[i] += evs[i].elapsed_time(evs[i + 1])
+    return {n: v / steps for n, v in zip(names, sums)}
+
+
+def cpu_baseline(inp, n_tokens, runs, torch):
+    import oracle
+    s = inp.shape
+    n_tokens = min(n_tokens, inp.x.shape[0])
+    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    x = inp.x[:n_tokens].cpu()
+    logits = inp.logits[:n_tokens].cpu()
+    wgu = inp.w_gate_up.cpu().float()        # upcast from bf16 exactly, outside the timing
+    wd = inp.w_down.cpu().float()
+    fwd = lambda: oracle.moe_forward(x, logits, s.top_k, wgu, wd, s.renormalize)
+    fwd()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fwd()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": n_tokens / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"first {n_tokens} of the {inp.x.shape[0]} prefill tokens, fp32 PyTorch oracle, "
+                      f"median of {runs} runs after 1 warm-up ({t:.2f} s each); cpu: {model}; "
+                      f"os.cpu_count()={os.cpu_count()}"}
+
+
+def traffic_from_profiles(kernel_tag):
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(kernel_tag)
+    except (ValueError, OSError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the MoE expert path is built and measured on a single "
+              "MI355X (multi-GPU expert parallelism is out of scope); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from easyinfra_amd import ops
+    from easyinfra_amd.workloads import MIXTRAL_8X7B, make_inputs, layer_flops, layer_bytes
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    shape = MIXTRAL_8X7B
+    T = args.tokens
+    inp = make_inputs(shape, T, device=dev)
+    H, I, k = shape.hidden, shape.inter, shape.top_k
+    n_local = inp.w_gate_up.shape[0]
+    ws = torch.empty(ops.fused_moe_workspace_bytes(T, H, I, shape.n_experts, k, n_local), dtype=torch.uint8,
+                     device=dev)
+
+    def layer():
+        ops.fused_moe(inp.x, inp.logits, k, inp.w_gate_up, inp.w_down, renormalize=shape.renormalize,
+                      workspace=ws)
+
+    ms = timed(layer, args.steps, args.warmup, torch)
+    A = T * k
+    flops = layer_flops(A, T, H, I)
+    stages = stage_times(inp, args.steps, args.warmup, torch, ops)
+    gu_flops = 4.0 * A * H * I
+    gu_ms = stages["gate_up_silu"]
+    achieved = gu_flops / (gu_ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": "grouped_gemm_kernel<256,256,...,silu> (gate/up + SiLU*mul)",
+            "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic_from_profiles("gate_up_silu_prefill"),
+            "flops_per_launch": gu_flops, "mean_launch_ms": round(gu_ms, 4)}
+
+    # decode batch (HBM-bound): the first decode-tokens rows of the same layer
+    Td = args.decode_tokens
+    dx, dl = inp.x[:Td].contiguous(), inp.logits[:Td].contiguous()
+    dws = torch.empty(ops.fused_moe_workspace_bytes(Td, H, I, shape.n_experts, k, n_local), dtype=torch.uint8,
+                      device=dev)
+    ids_d, _ = ops.router_topk(dl, k, shape.renormalize)
+    touched = int(torch.unique(ids_d).numel())
+    dms = timed(lambda: ops.fused_moe(dx, dl, k, inp.w_gate_up, inp.w_down, renormalize=shape.renormalize,
+                                      workspace=dws), max(args.steps, 20), args.warmup, torch)
+    dbytes = layer_bytes(touched, Td, shape.n_experts, H, I, 2, 2, 2)
+    decode = {"tokens": Td, "ms": round(dms, 4), "tokens_per_s": round(Td / (dms * 1e-3), 1),
+              "hbm_GBps": round(dbytes / (dms * 1e-3) / 1e9, 1),
+              "hbm_frac": round(dbytes / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "touched_experts": touched}
+
+    cpu = None
+    if args.cpu_tokens > 0:
+        cpu = cpu_baseline(inp, args.cpu_tokens, args.cpu_runs, torch)
+
+    line = {
+        "metric": METRIC, "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, router logits x@gate_w)",
+        "config": {"workload": "Mixtral-8x7B-shape MoE layer prefill", "tokens": T, "hidden": H, "inter": I,
+                   "experts": shape.n_experts, "top_k": k, "router": "softmax, top-2, renormalised",
+                   "weights": "bf16", "parallelism": "single GPU"},
+        "layer": {"tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                  "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                  "gflop": round(flops / 1e9, 1)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "decode": decode,
+        "kernels_ms": {k_: round(v, 4) for k_, v in stages.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

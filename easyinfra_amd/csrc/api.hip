@@ -1,0 +1,433 @@
+// C-ABI entry points (declared in include/eimoe.h): host-side validation, then
+// stream-ordered launches.  No device allocation, no host synchronisation.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/eimoe.h"
+#include "common.h"
+#include "kernels.h"
+
+using namespace eimoe;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(EIMOE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  g_err[0] = '\0';
+  return EIMOE_OK;
+}
+
+#define REQUIRE_PTR(p)                                                      \
+  do {                                                                      \
+    if ((p) == nullptr) return fail(EIMOE_ERR_NULL, "%s is NULL", #p);      \
+  } while (0)
+
+inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+int elem_size(int dt) { return dt == EIMOE_F32 ? 4 : dt == EIMOE_BF16 ? 2 : dt == EIMOE_FP8 ? 1 : 0; }
+
+int check_gemm_common(int max_rows, int n_seg, int e_mod) {
+  if (max_rows < 0) return fail(EIMOE_ERR_SHAPE, "max_rows=%d < 0", max_rows);
+  if (n_seg < 1 || n_seg > EIMOE_MAX_SEGMENTS)
+    return fail(EIMOE_ERR_SHAPE, "n_seg=%d outside [1,%d]", n_seg, EIMOE_MAX_SEGMENTS);
+  if (e_mod < 1) return fail(EIMOE_ERR_SHAPE, "e_mod=%d < 1", e_mod);
+  return EIMOE_OK;
+}
+
+int check_tile(int tile, int epi, int N) {
+  if (tile < EIMOE_TILE_AUTO || tile > EIMOE_TILE_16x64) return fail(EIMOE_ERR_SHAPE, "tile=%d unknown", tile);
+  if (tile != EIMOE_TILE_AUTO) {
+    const int oc = gemm_out_cols_per_tile(tile, epi);
+    if (N % oc != 0) return fail(EIMOE_ERR_ALIGN, "N=%d not a multiple of the tile's %d output columns", N, oc);
+  }
+  return EIMOE_OK;
+}
+
+// Split of the down projection's K so that small (decode) launches still fill the GPU.
+int pick_down_split(int max_rows, int n_local, int H, int I) {
+  const int tile = gemm_pick_tile(kEpiStoreF32, max_rows, n_local, H);
+  const int bm = tile == kTileL ? 256 : tile == kTileM ? 128 : tile == kTileS ? 32 : 16;
+  const long long mt = std::min<long long>(n_local, max_rows) + max_rows / bm;
+  const long long tiles = mt * (H / gemm_out_cols_per_tile(tile, kEpiStoreF32));
+  int split = 1;
+  while (split < 8 && tiles * split < 2 * kNumCu && (I % (64 * split * 2)) == 0) split *= 2;
+  return split;
+}
+
+struct FusedLayout {
+  size_t ids, w, counts, offsets, sorted_flat, sorted_tok, pos, h, y, sh_off, sh_h, sh_y, total;
+  int k_split;
+  int y_dtype;
+};
+
+FusedLayout fused_layout(int T, int H, int I, int k, int n_local, int Is, int out_dtype, int flags) {
+  FusedLayout L{};
+  const size_t A = static_cast<size_t>(T) * k;
+  L.y_dtype = ((flags & EIMOE_Y_F32) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
+  L.k_split = pick_down_split(static_cast<int>(A), n_local, H, I);
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align256(bytes);
+    return at;
+  };
+  L.ids = take(A * 4);
+  L.w = take(A * 4);
+  L.counts = take(static_cast<size_t>(n_local) * 4);
+  L.offsets = take(static_cast<size_t>(n_local + 1) * 4);
+  L.sorted_flat = take(A * 4);
+  L.sorted_tok = take(A * 4);
+  L.pos = take(A * 4);
+  L.h = take(A * I * 2);
+  L.y = take(static_cast<size_t>(L.k_split) * A * H * elem_size(L.y_dtype));
+  if (Is > 0) {
+    L.sh_off = take(2 * 4);
+    L.sh_h = take(static_cast<size_t>(T) * Is * 2);
+    L.sh_y = take(static_cast<size_t>(T) * H * elem_size(L.y_dtype));
+  }
+  L.total = o;
+  return L;
+}
+
+__global__ void dense_segment_kernel(int32_t* off, int T) {
+  if (threadIdx.x == 0) {
+    off[0] = 0;
+    off[1] = T;
+  }
+}
+
+int run_gate_up(const void* a, const int32_t* a_rows, int lda, const void* w, int w_dtype, const float* w_scale,
+                int H, int I, const int32_t* seg, int n_seg, int e_mod, int max_rows, void* h, int tile,
+                hipStream_t s) {
+  GemmArgs p{};
+  p.a = a;
+  p.a_rows = a_rows;
+  p.lda = lda;
+  p.b = w;
+  p.b_estride = 2ll * I * H;
+  p.ldb = H;
+  p.b_scale = w_scale;
+  p.nb_rows = 2 * I;
+  p.N = I;
+  p.K = H;
+  p.up_off = I;
+  p.seg_off = seg;
+  p.S = n_seg;
+  p.e_mod = e_mod;
+  p.c = h;
+  p.ldc = I;
+  p.c_split_stride = 0;
+  p.k_split = 1;
+  p.max_rows = max_rows;
+  return hip_check(launch_grouped_gemm(p, kEpiSiluBF16, w_dtype == EIMOE_FP8, max_rows, tile, s), "gate_up gemm");
+}
+
+int run_down(const void* h, int I, const void* w, int w_dtype, const float* w_scale, int H, const int32_t* seg,
+             int n_seg, int e_mod, int max_rows, void* y, int y_dtype, int k_split, int tile, hipStream_t s) {
+  GemmArgs p{};
+  p.a = h;
+  p.a_rows = nullptr;
+  p.lda = I;
+  p.b = w;
+  p.b_estride = static_cast<long long>(H) * I;
+  p.ldb = I;
+  p.b_scale = w_scale;
+  p.nb_rows = H;
+  p.N = H;
+  p.K = I / k_split;
+  p.up_off = 0;
+  p.seg_off = seg;
+  p.S = n_seg;
+  p.e_mod = e_mod;
+  p.c = y;
+  p.ldc = H;
+  p.c_split_stride = static_cast<long long>(max_rows) * H;
+  p.k_split = k_split;
+  p.max_rows = max_rows;
+  const int epi = y_dtype == EIMOE_F32 ? kEpiStoreF32 : kEpiStoreBF16;
+  return hip_check(launch_grouped_gemm(p, epi, w_dtype == EIMOE_FP8, max_rows, tile, s), "down gemm");
+}
+
+}  // namespace
+
+extern "C" {
+
+int eimoe_abi_version(void) { return EIMOE_ABI_VERSION; }
+
+const char* eimoe_last_error(void) { return g_err; }
+
+int eimoe_router_topk(const float* logits, int T, int E, int k, int renormalize, int32_t* topk_ids,
+                      float* topk_weights, void* stream) {
+  if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
+  if (E < 1 || E > EIMOE_MAX_EXPERTS) return fail(EIMOE_ERR_SHAPE, "E=%d outside [1,%d]", E, EIMOE_MAX_EXPERTS);
+  if (k < 1 || k > E || k > EIMOE_MAX_TOPK)
+    return fail(EIMOE_ERR_SHAPE, "k=%d outside [1,min(E=%d,%d)]", k, E, EIMOE_MAX_TOPK);
+  if (T == 0) return EIMOE_OK;
+  REQUIRE_PTR(logits);
+  REQUIRE_PTR(topk_ids);
+  REQUIRE_PTR(topk_weights);
+  return hip_check(launch_router_topk(logits, T, E, k, renormalize ? 1 : 0, topk_ids, topk_weights, S(stream)),
+                   "router_topk");
+}
+
+int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, int32_t* counts, int32_t* offsets,
+                int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream) {
+  if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
+  if (k < 1 || k > EIMOE_MAX_TOPK) return fail(EIMOE_ERR_SHAPE, "k=%d outside [1,%d]", k, EIMOE_MAX_TOPK);
+  if (n_local < 1 || n_local > EIMOE_MAX_EXPERTS)
+    return fail(EIMOE_ERR_SHAPE, "n_local=%d outside [1,%d]", n_local, EIMOE_MAX_EXPERTS);
+  if (e_lo < 0) return fail(EIMOE_ERR_SHAPE, "e_lo=%d < 0", e_lo);
+  if (static_cast<long long>(T) * k > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "T*k overflows int32");
+  REQUIRE_PTR(counts);
+  REQUIRE_PTR(offsets);
+  if (T > 0) {
+    REQUIRE_PTR(topk_ids);
+    REQUIRE_PTR(sorted_flat);
+    REQUIRE_PTR(sorted_tok);
+    REQUIRE_PTR(pos);
+  }
+  return hip_check(launch_align(topk_ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos,
+                                S(stream)),
+                   "align");
+}
+
+int eimoe_counts_to_offsets(const int32_t* counts, int n_seg, int32_t* offsets, void* stream) {
+  if (n_seg < 1 || n_seg > EIMOE_MAX_SEGMENTS)
+    return fail(EIMOE_ERR_SHAPE, "n_seg=%d outside [1,%d]", n_seg, EIMOE_MAX_SEGMENTS);
+  REQUIRE_PTR(counts);
+  REQUIRE_PTR(offsets);
+  return hip_check(launch_counts_to_offsets(counts, n_seg, offsets, S(stream)), "counts_to_offsets");
+}
+
+int eimoe_gather(const void* x, int dtype, int H, const int32_t* rows, const int32_t* num_rows, int max_rows,
+                 void* xs, void* stream) {
+  if (dtype != EIMOE_F32 && dtype != EIMOE_BF16) return fail(EIMOE_ERR_DTYPE, "gather dtype=%d", dtype);
+  if (H < 1) return fail(EIMOE_ERR_SHAPE, "H=%d < 1", H);
+  const int row_bytes = H * elem_size(dtype);
+  if (row_bytes % 16) return fail(EIMOE_ERR_ALIGN, "row bytes %d not a multiple of 16", row_bytes);
+  if (max_rows < 0) return fail(EIMOE_ERR_SHAPE, "max_rows=%d < 0", max_rows);
+  if (max_rows == 0) return EIMOE_OK;
+  REQUIRE_PTR(x);
+  REQUIRE_PTR(rows);
+  REQUIRE_PTR(num_rows);
+  REQUIRE_PTR(xs);
+  return hip_check(launch_gather_rows(x, row_bytes, rows, num_rows, max_rows, xs, S(stream)), "gather");
+}
+
+int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int lda, const void* w_gate_up, int w_dtype,
+                            const float* w_scale, int H, int I, const int32_t* seg_offsets, int n_seg, int e_mod,
+                            int max_rows, void* h, int tile, void* stream) {
+  int rc = check_gemm_common(max_rows, n_seg, e_mod);
+  if (rc) return rc;
+  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
+  if (H < 64 || H % 64) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 64", H);
+  if (I < 32 || I % 32) return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 32", I);
+  if (lda < H) return fail(EIMOE_ERR_SHAPE, "lda=%d < H=%d", lda, H);
+  if (lda % 8) return fail(EIMOE_ERR_ALIGN, "lda=%d must be a multiple of 8", lda);
+  if ((rc = check_tile(tile, kEpiSiluBF16, I))) return rc;
+  if (max_rows == 0) return EIMOE_OK;
+  REQUIRE_PTR(a);
+  REQUIRE_PTR(w_gate_up);
+  REQUIRE_PTR(seg_offsets);
+  REQUIRE_PTR(h);
+  if (w_dtype == EIMOE_FP8) REQUIRE_PTR(w_scale);
+  return run_gate_up(a, a_rows, lda, w_gate_up, w_dtype, w_scale, H, I, seg_offsets, n_seg, e_mod, max_rows, h, tile,
+                     S(stream));
+}
+
+int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const float* w_scale, int H,
+                    const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows, void* y, int y_dtype,
+                    int k_split, int tile, void* stream) {
+  int rc = check_gemm_common(max_rows, n_seg, e_mod);
+  if (rc) return rc;
+  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
+  if (y_dtype != EIMOE_BF16 && y_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "y_dtype=%d", y_dtype);
+  if (H < 64 || H % 64) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 64", H);
+  if (k_split < 1 || k_split > 64) return fail(EIMOE_ERR_SHAPE, "k_split=%d outside [1,64]", k_split);
+  if (I < 64 || I % (64 * k_split))
+    return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 64*k_split=%d", I, 64 * k_split);
+  if ((rc = check_tile(tile, kEpiStoreF32, H))) return rc;
+  if (max_rows == 0) return EIMOE_OK;
+  REQUIRE_PTR(h);
+  REQUIRE_PTR(w_down);
+  REQUIRE_PTR(seg_offsets);
+  REQUIRE_PTR(y);
+  if (w_dtype == EIMOE_FP8) REQUIRE_PTR(w_scale);
+  return run_down(h, I, w_down, w_dtype, w_scale, H, seg_offsets, n_seg, e_mod, max_rows, y, y_dtype, k_split, tile,
+                  S(stream));
+}
+
+int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int lda, const void* b, int b_dtype,
+                       const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
+                       int n_seg, int e_mod, int max_rows, void* c, int c_dtype, int tile, void* stream) {
+  int rc = check_gemm_common(max_rows, n_seg, e_mod);
+  if (rc) return rc;
+  if (b_dtype != EIMOE_BF16 && b_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "b_dtype=%d", b_dtype);
+  if (c_dtype != EIMOE_BF16 && c_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "c_dtype=%d", c_dtype);
+  if (K < 64 || K % 64) return fail(EIMOE_ERR_ALIGN, "K=%d must be a positive multiple of 64", K);
+  if (N < 64 || N % 64) return fail(EIMOE_ERR_ALIGN, "N=%d must be a positive multiple of 64", N);
+  if (lda < K || lda % 8) return fail(EIMOE_ERR_SHAPE, "lda=%d must be >= K=%d and a multiple of 8", lda, K);
+  if (b_expert_stride < static_cast<long long>(N) * K)
+    return fail(EIMOE_ERR_SHAPE, "b_expert_stride=%lld < N*K", b_expert_stride);
+  if ((rc = check_tile(tile, kEpiStoreF32, N))) return rc;
+  if (max_rows == 0) return EIMOE_OK;
+  REQUIRE_PTR(a);
+  REQUIRE_PTR(b);
+  REQUIRE_PTR(seg_offsets);
+  REQUIRE_PTR(c);
+  if (b_dtype == EIMOE_FP8) REQUIRE_PTR(b_scale);
+  GemmArgs p{};
+  p.a = a;
+  p.a_rows = a_rows;
+  p.lda = lda;
+  p.b = b;
+  p.b_estride = b_expert_stride;
+  p.ldb = K;
+  p.b_scale = b_scale;
+  p.nb_rows = N;
+  p.N = N;
+  p.K = K;
+  p.seg_off = seg_offsets;
+  p.S = n_seg;
+  p.e_mod = e_mod;
+  p.c = c;
+  p.ldc = N;
+  p.k_split = 1;
+  p.max_rows = max_rows;
+  const int epi = c_dtype == EIMOE_F32 ? kEpiStoreF32 : kEpiStoreBF16;
+  return hip_check(launch_grouped_gemm(p, epi, b_dtype == EIMOE_FP8, max_rows, tile, S(stream)), "grouped_gemm");
+}
+
+int eimoe_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
+                  const float* topk_weights, int T, int k, int H, const void* shared_y, int shared_dtype, void* out,
+                  int out_dtype, void* stream) {
+  if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
+  if (k < 1 || k > EIMOE_MAX_TOPK) return fail(EIMOE_ERR_SHAPE, "k=%d outside [1,%d]", k, EIMOE_MAX_TOPK);
+  if (H < 8 || H % 8) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 8", H);
+  if (n_split < 1) return fail(EIMOE_ERR_SHAPE, "n_split=%d < 1", n_split);
+  if (y_dtype != EIMOE_F32 && y_dtype != EIMOE_BF16) return fail(EIMOE_ERR_DTYPE, "y_dtype=%d", y_dtype);
+  if (out_dtype != EIMOE_F32 && out_dtype != EIMOE_BF16) return fail(EIMOE_ERR_DTYPE, "out_dtype=%d", out_dtype);
+  if (shared_y && shared_dtype != EIMOE_F32 && shared_dtype != EIMOE_BF16)
+    return fail(EIMOE_ERR_DTYPE, "shared_dtype=%d", shared_dtype);
+  if (T == 0) return EIMOE_OK;
+  REQUIRE_PTR(y);
+  REQUIRE_PTR(pos);
+  REQUIRE_PTR(topk_weights);
+  REQUIRE_PTR(out);
+  return hip_check(launch_combine(y, y_dtype, n_split, split_stride, pos, topk_weights, T, k, H, shared_y,
+                                  shared_dtype, out, out_dtype, S(stream)),
+                   "combine");
+}
+
+int eimoe_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,
+                            void* stream) {
+  if (dtype != EIMOE_F32 && dtype != EIMOE_BF16) return fail(EIMOE_ERR_DTYPE, "dtype=%d", dtype);
+  if (rows < 0 || cols < 1) return fail(EIMOE_ERR_SHAPE, "rows=%lld cols=%d", rows, cols);
+  if (rows == 0) return EIMOE_OK;
+  REQUIRE_PTR(x);
+  REQUIRE_PTR(q);
+  REQUIRE_PTR(scale);
+  return hip_check(launch_quantize_rows_fp8(x, dtype, rows, cols, q, scale, S(stream)), "quantize_rows_fp8");
+}
+
+size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_local, int shared_inter,
+                                       int out_dtype, int flags) {
+  (void)E;
+  if (T < 0 || H < 1 || I < 1 || k < 1 || n_local < 1 || shared_inter < 0) return 0;
+  return fused_layout(T, H, I, k, n_local, shared_inter, out_dtype, flags).total;
+}
+
+int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int E, int k, const void* w_gate_up,
+                    const void* w_down, int w_dtype, const float* w_gate_up_scale, const float* w_down_scale, int e_lo,
+                    int n_local, const void* shared_gate_up, const void* shared_down, int shared_inter, int flags,
+                    void* out, int out_dtype, void* workspace, size_t workspace_bytes, int32_t* topk_ids_out,
+                    float* topk_w_out, void* stream) {
+  if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
+  if (E < 1 || E > EIMOE_MAX_EXPERTS) return fail(EIMOE_ERR_SHAPE, "E=%d outside [1,%d]", E, EIMOE_MAX_EXPERTS);
+  if (k < 1 || k > E || k > EIMOE_MAX_TOPK)
+    return fail(EIMOE_ERR_SHAPE, "k=%d outside [1,min(E=%d,%d)]", k, E, EIMOE_MAX_TOPK);
+  if (n_local < 1 || e_lo < 0 || e_lo + n_local > E)
+    return fail(EIMOE_ERR_SHAPE, "expert window [%d,%d) not inside [0,%d)", e_lo, e_lo + n_local, E);
+  if (H < 64 || H % 64) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 64", H);
+  if (I < 64 || I % 64) return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 64", I);
+  if (shared_inter < 0 || (shared_inter > 0 && shared_inter % 64))
+    return fail(EIMOE_ERR_ALIGN, "shared_inter=%d must be a multiple of 64", shared_inter);
+  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
+  if (out_dtype != EIMOE_BF16 && out_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "out_dtype=%d", out_dtype);
+  if (static_cast<long long>(T) * k > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "T*k overflows int32");
+  if (T == 0) return EIMOE_OK;
+  REQUIRE_PTR(x);
+  REQUIRE_PTR(logits);
+  REQUIRE_PTR(w_gate_up);
+  REQUIRE_PTR(w_down);
+  REQUIRE_PTR(out);
+  REQUIRE_PTR(workspace);
+  if (w_dtype == EIMOE_FP8) {
+    REQUIRE_PTR(w_gate_up_scale);
+    REQUIRE_PTR(w_down_scale);
+  }
+  if (shared_inter > 0) {
+    REQUIRE_PTR(shared_gate_up);
+    REQUIRE_PTR(shared_down);
+  }
+  const FusedLayout L = fused_layout(T, H, I, k, n_local, shared_inter, out_dtype, flags);
+  if (workspace_bytes < L.total)
+    return fail(EIMOE_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  auto at = [&](size_t off) { return static_cast<void*>(ws + off); };
+  int32_t* ids = topk_ids_out ? topk_ids_out : static_cast<int32_t*>(at(L.ids));
+  float* w = topk_w_out ? topk_w_out : static_cast<float*>(at(L.w));
+  int32_t* counts = static_cast<int32_t*>(at(L.counts));
+  int32_t* offsets = static_cast<int32_t*>(at(L.offsets));
+  int32_t* sorted_flat = static_cast<int32_t*>(at(L.sorted_flat));
+  int32_t* sorted_tok = static_cast<int32_t*>(at(L.sorted_tok));
+  int32_t* pos = static_cast<int32_t*>(at(L.pos));
+  const hipStream_t s = S(stream);
+  const int A = T * k;
+  int rc;
+  if ((rc = hip_check(launch_router_topk(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, ids, w, s),
+                      "router_topk")))
+    return rc;
+  if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos, s),
+                      "align")))
+    return rc;
+  if ((rc = run_gate_up(x, sorted_tok, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local, A,
+                        at(L.h), EIMOE_TILE_AUTO, s)))
+    return rc;
+  if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y), L.y_dtype,
+                     L.k_split, EIMOE_TILE_AUTO, s)))
+    return rc;
+  const void* sh_y = nullptr;
+  if (shared_inter > 0) {
+    int32_t* sh_off = static_cast<int32_t*>(at(L.sh_off));
+    hipLaunchKernelGGL(dense_segment_kernel, dim3(1), dim3(64), 0, s, sh_off, T);
+    if ((rc = hip_check(hipGetLastError(), "shared offsets"))) return rc;
+    if ((rc = run_gate_up(x, nullptr, H, shared_gate_up, EIMOE_BF16, nullptr, H, shared_inter, sh_off, 1, 1, T,
+                          at(L.sh_h), EIMOE_TILE_AUTO, s)))
+      return rc;
+    if ((rc = run_down(at(L.sh_h), shared_inter, shared_down, EIMOE_BF16, nullptr, H, sh_off, 1, 1, T, at(L.sh_y),
+                       L.y_dtype, 1, EIMOE_TILE_AUTO, s)))
+      return rc;
+    sh_y = at(L.sh_y);
+  }
+  return hip_check(launch_combine(at(L.y), L.y_dtype, L.k_split, static_cast<long long>(A) * H, pos, w, T, k, H, sh_y,
+                                  L.y_dtype, out, out_dtype, s),
+                   "combine");
+}
+
+}  // extern "C"

@@ -1,0 +1,58 @@
+// Internal launcher declarations shared by the kernel files and the C-ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace eimoe {
+
+constexpr int kMaxSeg = 1024;  // segments (local experts x source ranks) per grouped GEMM
+
+enum Epilogue : int { kEpiStoreF32 = 0, kEpiStoreBF16 = 1, kEpiSiluBF16 = 2 };
+
+// One grouped GEMM launch: for each segment s (rows [seg_off[s], seg_off[s+1]) of A),
+// C[rows, :] = A[rows, :] . B[s % e_mod]^T  (B in nn.Linear layout [N_b, K]).
+struct GemmArgs {
+  const void* a;             // bf16 [*, lda]
+  const int32_t* a_rows;     // optional gather map: logical row r reads a[a_rows[r]]
+  long long lda;
+  const void* b;             // bf16 or fp8-e4m3 [E][N_b][K]
+  long long b_estride;       // elements between experts
+  long long ldb;
+  const float* b_scale;      // fp8: per-output-channel scale [E][N_b]; null for bf16
+  int nb_rows;               // N_b, rows per expert in b (scale indexing)
+  int N;                     // output columns (silu: I)
+  int K;                     // reduction length per split
+  int up_off;                // silu: first 'up' row in b (= I)
+  const int32_t* seg_off;    // [S+1] device
+  int S;
+  int e_mod;
+  void* c;
+  long long ldc;
+  long long c_split_stride;  // elements between split-K partial outputs
+  int k_split;
+  int max_rows;              // rows of A (non-gathered) / of C; segment bounds are clamped to it
+};
+
+// Tile shape selector; the launcher maps it to a kernel instantiation.
+enum TileCfg : int { kTileAuto = 0, kTileL = 1, kTileM = 2, kTileS = 3, kTileXS = 4 };
+
+hipError_t launch_router_topk(const float* logits, int T, int E, int k, int renorm, int32_t* ids, float* w,
+                              hipStream_t s);
+size_t align_lds_bytes(int n_loc);
+hipError_t launch_align(const int32_t* ids, int T, int k, int e_lo, int n_loc, int32_t* counts, int32_t* offsets,
+                        int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, hipStream_t s);
+hipError_t launch_counts_to_offsets(const int32_t* counts, int S, int32_t* offsets, hipStream_t s);
+hipError_t launch_gather_rows(const void* x, int row_bytes, const int32_t* rows, const int32_t* num_rows,
+                              int max_rows, void* xs, hipStream_t s);
+hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
+                          const float* w, int T, int k, int H, const void* shared_y, int shared_dtype, void* out,
+                          int out_dtype, hipStream_t s);
+// epi: Epilogue; b_fp8: B is e4m3; max_rows bounds the grid; tile: TileCfg.
+hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, int max_rows, int tile, hipStream_t s);
+int gemm_pick_tile(int epi, int max_rows, int S, int N);
+int gemm_out_cols_per_tile(int tile, int epi);
+hipError_t launch_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,
+                                    hipStream_t s);
+
+}  // namespace eimoe

@@ -1,0 +1,131 @@
+// Row gather into expert-contiguous order, and the weighted top-k combine.
+//
+// gather  replaces send_hidden_states = h[send_indices] (moe_all2all.py:351).
+// combine replaces _all2all_chunk_output_compute (moe_all2all.py:291-307):
+//   out = zeros[T,H]; out.index_add_(0, token, y * w[:,None])
+// as a token-major gather-reduce through the inverse permutation ``pos``: each
+// output row is written once, accumulated in fp32 in slot order, no atomics, so
+// the result is deterministic run to run.  Optional extras fused into the same
+// pass: split-K partial outputs of the down projection (summed before weighting),
+// and the shared-expert output (weight 1.0, moe_all2all.py:535-537).
+#include "common.h"
+#include "kernels.h"
+
+namespace eimoe {
+
+__device__ __forceinline__ void load8(const void* base, int dtype, long long off, float* v) {
+  if (dtype == kBF16) {
+    const u32x4_t q = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(base) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(q[i] << 16);
+      v[2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
+    }
+  } else {
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(static_cast<const float*>(base) + off);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(static_cast<const float*>(base) + off + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
+}
+
+__device__ __forceinline__ void store8(void* base, int dtype, long long off, const float* v) {
+  if (dtype == kBF16) {
+    u32x4_t q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(base) + off) = q;
+  } else {
+    f32x4_t a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = v[i];
+      b[i] = v[4 + i];
+    }
+    *reinterpret_cast<f32x4_t*>(static_cast<float*>(base) + off) = a;
+    *reinterpret_cast<f32x4_t*>(static_cast<float*>(base) + off + 4) = b;
+  }
+}
+
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint8_t* __restrict__ x, int row_bytes,
+                                                          const int32_t* __restrict__ rows,
+                                                          const int32_t* __restrict__ num_rows, int max_rows,
+                                                          uint8_t* __restrict__ xs) {
+  const int n = min(*num_rows, max_rows);
+  const int cpr = row_bytes / 16;
+  const long long total = static_cast<long long>(n) * cpr;
+  for (long long i = blockIdx.x * 256ll + threadIdx.x; i < total; i += static_cast<long long>(gridDim.x) * 256) {
+    const int r = static_cast<int>(i / cpr);
+    const int c = static_cast<int>(i % cpr);
+    const long long src = static_cast<long long>(rows[r]) * row_bytes + c * 16;
+    *reinterpret_cast<u32x4_t*>(xs + static_cast<long long>(r) * row_bytes + c * 16) =
+        *reinterpret_cast<const u32x4_t*>(x + src);
+  }
+}
+
+hipError_t launch_gather_rows(const void* x, int row_bytes, const int32_t* rows, const int32_t* num_rows,
+                              int max_rows, void* xs, hipStream_t s) {
+  const long long total = static_cast<long long>(max_rows) * (row_bytes / 16);
+  long long blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,
+                     static_cast<const uint8_t*>(x), row_bytes, rows, num_rows, max_rows, static_cast<uint8_t*>(xs));
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y, int y_dtype, int n_split,
+                                                      long long split_stride, const int32_t* __restrict__ pos,
+                                                      const float* __restrict__ w, int T, int k, int H,
+                                                      const void* __restrict__ shared_y, int shared_dtype,
+                                                      void* __restrict__ out, int out_dtype) {
+  const int cpr = H / 8;
+  const long long total = static_cast<long long>(T) * cpr;
+  for (long long i = blockIdx.x * 256ll + threadIdx.x; i < total; i += static_cast<long long>(gridDim.x) * 256) {
+    const int t = static_cast<int>(i / cpr);
+    const int h = static_cast<int>(i % cpr) * 8;
+    float acc[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const int p = pos[static_cast<long long>(t) * k + j];
+      if (p < 0) continue;
+      const float wj = w[static_cast<long long>(t) * k + j];
+      float ys[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ys[q] = 0.f;
+      for (int s = 0; s < n_split; ++s) {
+        float v[8];
+        load8(y, y_dtype, s * split_stride + static_cast<long long>(p) * H + h, v);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ys[q] += v[q];
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] += wj * ys[q];
+    }
+    if (shared_y) {
+      float v[8];
+      load8(shared_y, shared_dtype, static_cast<long long>(t) * H + h, v);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] += v[q];
+    }
+    store8(out, out_dtype, static_cast<long long>(t) * H + h, acc);
+  }
+}
+
+hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
+                          const float* w, int T, int k, int H, const void* shared_y, int shared_dtype, void* out,
+                          int out_dtype, hipStream_t s) {
+  const long long total = static_cast<long long>(T) * (H / 8);
+  long long blocks = (total + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, y, y_dtype, n_split,
+                     split_stride, pos, w, T, k, H, shared_y, shared_dtype, out, out_dtype);
+  return hipGetLastError();
+}
+
+}  // namespace eimoe

@@ -1,0 +1,245 @@
+"""Torch-facing wrappers of the HIP kernels (one per C-ABI entry point).
+
+Tensors must already live on the GPU; each call enqueues on the current torch
+stream and returns fresh output tensors (the reference's ``new_empty`` outputs,
+fused_moe.py:444, 464).  Nothing here synchronises the device or falls back to
+PyTorch math: a missing library or an unsupported shape raises.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+_DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float8_e4m3fn: _lib.FP8}
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _req(t: torch.Tensor, name: str, dtype=None, dim=None):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype not in (dtype if isinstance(dtype, tuple) else (dtype,)):
+        raise TypeError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if dim is not None and t.dim() != dim:
+        raise ValueError(f"{name} must be {dim}-D, got {tuple(t.shape)}")
+
+
+def router_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+    """modeling_qwen3_moe.py:255-266 -> (ids int32 [T,k], weights fp32 [T,k])."""
+    _req(logits, "logits", torch.float32, 2)
+    T, E = logits.shape
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=logits.device)
+    w = torch.empty(T, top_k, dtype=torch.float32, device=logits.device)
+    call("eimoe_router_topk", logits.data_ptr(), T, E, top_k, int(renormalize), ids.data_ptr(), w.data_ptr(),
+         _stream(logits))
+    return ids, w
+
+
+def align(topk_ids: torch.Tensor, n_local: int, e_lo: int = 0) -> dict:
+    """Counts/offsets/stable permutation (blocks/moe/base.py:343-364, moe_all2all.py:346-348)."""
+    _req(topk_ids, "topk_ids", torch.int32, 2)
+    T, k = topk_ids.shape
+    dev = topk_ids.device
+    A = T * k
+    out = {
+        "counts": torch.empty(n_local, dtype=torch.int32, device=dev),
+        "offsets": torch.empty(n_local + 1, dtype=torch.int32, device=dev),
+        "sorted_flat": torch.empty(A, dtype=torch.int32, device=dev),
+        "sorted_tok": torch.empty(A, dtype=torch.int32, device=dev),
+        "pos": torch.empty(A, dtype=torch.int32, device=dev),
+    }
+    call("eimoe_align", topk_ids.data_ptr(), T, k, e_lo, n_local, out["counts"].data_ptr(),
+         out["offsets"].data_ptr(), out["sorted_flat"].data_ptr(), out["sorted_tok"].data_ptr(),
+         out["pos"].data_ptr(), _stream(topk_ids))
+    return out
+
+
+def counts_to_offsets(counts: torch.Tensor) -> torch.Tensor:
+    _req(counts, "counts", torch.int32, 1)
+    off = torch.empty(counts.numel() + 1, dtype=torch.int32, device=counts.device)
+    call("eimoe_counts_to_offsets", counts.data_ptr(), counts.numel(), off.data_ptr(), _stream(counts))
+    return off
+
+
+def gather(x: torch.Tensor, rows: torch.Tensor, num_rows: torch.Tensor, max_rows: int) -> torch.Tensor:
+    """xs[r] = x[rows[r]] for r < num_rows (a 1-element device tensor), moe_all2all.py:351."""
+    _req(x, "x", (torch.float32, torch.bfloat16), 2)
+    _req(rows, "rows", torch.int32)
+    xs = torch.empty(max_rows, x.shape[1], dtype=x.dtype, device=x.device)
+    call("eimoe_gather", x.data_ptr(), _dt(x), x.shape[1], rows.data_ptr(), num_rows.data_ptr(), max_rows,
+         xs.data_ptr(), _stream(x))
+    return xs
+
+
+def gemm_gate_up_silu(a: torch.Tensor, w_gate_up: torch.Tensor, seg_offsets: torch.Tensor, max_rows: int,
+                      a_rows: Optional[torch.Tensor] = None, w_scale: Optional[torch.Tensor] = None,
+                      e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
+    """fused_moe.py:445-459: h = silu(a.Wg^T) * (a.Wu^T) per segment -> bf16 [max_rows, I]."""
+    _req(a, "a", torch.bfloat16, 2)
+    _req(w_gate_up, "w_gate_up", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    _req(seg_offsets, "seg_offsets", torch.int32, 1)
+    E, I2, H = w_gate_up.shape
+    I = I2 // 2
+    if a.shape[1] != H:
+        raise ValueError(f"a has {a.shape[1]} columns, weights expect H={H}")
+    if a_rows is not None:
+        _req(a_rows, "a_rows", torch.int32)
+    if w_scale is not None:
+        _req(w_scale, "w_scale", torch.float32)
+    h = torch.empty(max_rows, I, dtype=torch.bfloat16, device=a.device)
+    call("eimoe_gemm_gate_up_silu", a.data_ptr(), _ptr(a_rows), a.stride(0), w_gate_up.data_ptr(), _dt(w_gate_up),
+         _ptr(w_scale), H, I, seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, h.data_ptr(),
+         tile, _stream(a))
+    return h
+
+
+def gemm_down(h: torch.Tensor, w_down: torch.Tensor, seg_offsets: torch.Tensor, max_rows: int,
+              out_dtype=torch.float32, k_split: int = 1, w_scale: Optional[torch.Tensor] = None,
+              e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
+    """fused_moe.py:463-476: y = h . Wd^T per segment -> [k_split, max_rows, H] partial planes."""
+    _req(h, "h", torch.bfloat16, 2)
+    _req(w_down, "w_down", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    _req(seg_offsets, "seg_offsets", torch.int32, 1)
+    E, H, I = w_down.shape
+    if h.shape[1] != I:
+        raise ValueError(f"h has {h.shape[1]} columns, weights expect I={I}")
+    y = torch.empty(k_split, max_rows, H, dtype=out_dtype, device=h.device)
+    call("eimoe_gemm_down", h.data_ptr(), I, w_down.data_ptr(), _dt(w_down), _ptr(w_scale), H,
+         seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, y.data_ptr(), _dt(y), k_split, tile,
+         _stream(h))
+    return y
+
+
+def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg_offsets: torch.Tensor, max_rows: int,
+                 out_dtype=torch.bfloat16, a_rows: Optional[torch.Tensor] = None,
+                 b_scale: Optional[torch.Tensor] = None, e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
+    """single_group_gemm_moe.py:76-91: c[rows_s] = a[rows_s] . b[s % e_mod]^T, b packed [E,N,K]."""
+    _req(a, "a", torch.bfloat16, 2)
+    _req(b, "b", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    _req(seg_offsets, "seg_offsets", torch.int32, 1)
+    E, N, K = b.shape
+    c = torch.empty(max_rows, N, dtype=out_dtype, device=a.device)
+    call("eimoe_grouped_gemm", a.data_ptr(), _ptr(a_rows), a.stride(0), b.data_ptr(), _dt(b), _ptr(b_scale),
+         N * K, N, K, seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, c.data_ptr(), _dt(c),
+         tile, _stream(a))
+    return c
+
+
+def combine(y: torch.Tensor, pos: torch.Tensor, topk_weights: torch.Tensor, shared_y: Optional[torch.Tensor] = None,
+            out_dtype=torch.bfloat16) -> torch.Tensor:
+    """moe_all2all.py:291-307 (+ shared-expert add): out[t] = sum_j w[t,j] * sum_s y[s][pos[t,j]]."""
+    if y.dim() == 2:
+        y = y.unsqueeze(0)
+    _req(y, "y", (torch.float32, torch.bfloat16), 3)
+    _req(topk_weights, "topk_weights", torch.float32, 2)
+    _req(pos, "pos", torch.int32)
+    T, k = topk_weights.shape
+    n_split, rows, H = y.shape
+    if shared_y is not None:
+        _req(shared_y, "shared_y", (torch.float32, torch.bfloat16), 2)
+    out = torch.empty(T, H, dtype=out_dtype, device=y.device)
+    call("eimoe_combine", y.data_ptr(), _dt(y), n_split, rows * H, pos.data_ptr(), topk_weights.data_ptr(), T, k, H,
+         _ptr(shared_y), _dt(shared_y) if shared_y is not None else 0, out.data_ptr(), _dt(out), _stream(y))
+    return out
+
+
+def quantize_rows_fp8(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row absmax/448 scale and e4m3fn values; rows = all leading dims."""
+    _req(x, "x", (torch.float32, torch.bfloat16))
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    call("eimoe_quantize_rows_fp8", x.data_ptr(), _dt(x), rows, cols, q.data_ptr(), s.data_ptr(), _stream(x))
+    return q, s
+
+
+def quantize_weights_fp8(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Expert weights [E,N,K] -> (e4m3fn [E,N,K], per-output-channel scales [E,N])."""
+    return quantize_rows_fp8(w)
+
+
+def fused_moe_workspace_bytes(T, H, I, E, k, n_local, shared_inter=0, out_dtype=torch.bfloat16, flags=0) -> int:
+    return int(_lib.lib().eimoe_fused_moe_workspace_bytes(T, H, I, E, k, n_local, shared_inter,
+                                                           _DT[out_dtype], flags))
+
+
+def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: int, w_gate_up: torch.Tensor,
+              w_down: torch.Tensor, *, renormalize: bool = True, shared_gate_up: Optional[torch.Tensor] = None,
+              shared_down: Optional[torch.Tensor] = None, expert_range: Optional[Sequence[int]] = None,
+              w_scales: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, out_dtype=None, y_fp32: bool = False,
+              workspace: Optional[torch.Tensor] = None, return_routing: bool = False):
+    """The MoE layer: (hidden_states [T,H], router_logits [T,E], top_k) -> combined output [T,H].
+
+    Reproduces MoeAll2AllBlock's stages at ep=1 (moe_all2all.py:85-95) with
+    FusedMoE.forward_ep (fused_moe.py:106-156) as the expert step:
+    route (softmax, top-k, optional renorm) -> align -> gate/up + SiLU*mul ->
+    down -> weighted combine (+ shared experts, weight 1).
+
+    ``expert_range=(lo, hi)``: only experts [lo, hi) of the router's E are resident
+    (one GPU's EP share); ``w_gate_up``/``w_down`` hold exactly those.  Tokens with
+    no resident expert produce zero rows.
+    ``w_scales=(s_gate_up [E,2I], s_down [E,H])`` marks fp8-e4m3 weights (W8A16).
+    fp32 hidden states are rounded to bf16 for the MFMA path.
+    """
+    x = hidden_states
+    if x.dtype == torch.float32:
+        x = x.to(torch.bfloat16)
+    _req(x, "hidden_states", torch.bfloat16, 2)
+    _req(router_logits, "router_logits", torch.float32, 2)
+    _req(w_gate_up, "w_gate_up", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    _req(w_down, "w_down", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    T, H = x.shape
+    E = router_logits.shape[1]
+    n_local, I2, H2 = w_gate_up.shape
+    I = I2 // 2
+    if H2 != H or tuple(w_down.shape) != (n_local, H, I):
+        raise ValueError(f"weight shapes {tuple(w_gate_up.shape)}/{tuple(w_down.shape)} do not match H={H}")
+    lo, hi = expert_range if expert_range is not None else (0, E)
+    if hi - lo != n_local:
+        raise ValueError(f"expert_range {lo, hi} holds {hi - lo} experts, weights hold {n_local}")
+    fp8 = w_gate_up.dtype == torch.float8_e4m3fn
+    if fp8 != (w_down.dtype == torch.float8_e4m3fn) or fp8 != (w_scales is not None):
+        raise ValueError("fp8 weights need both tensors in e4m3fn and w_scales=(s_gate_up, s_down)")
+    out_dtype = out_dtype or hidden_states.dtype
+    Is = 0
+    if shared_gate_up is not None:
+        _req(shared_gate_up, "shared_gate_up", torch.bfloat16, 2)
+        _req(shared_down, "shared_down", torch.bfloat16, 2)
+        Is = shared_down.shape[1]
+    flags = (_lib.RENORMALIZE if renormalize else 0) | (_lib.Y_F32 if y_fp32 else 0)
+    need = fused_moe_workspace_bytes(T, H, I, E, top_k, n_local, Is, out_dtype, flags)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty(T, H, dtype=out_dtype, device=x.device)
+    ids = w = None
+    if return_routing:
+        ids = torch.empty(T, top_k, dtype=torch.int32, device=x.device)
+        w = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
+    s_gu, s_d = w_scales if fp8 else (None, None)
+    call("eimoe_fused_moe", x.data_ptr(), router_logits.data_ptr(), T, H, I, E, top_k, w_gate_up.data_ptr(),
+         w_down.data_ptr(), _dt(w_gate_up), _ptr(s_gu), _ptr(s_d), lo, n_local, _ptr(shared_gate_up),
+         _ptr(shared_down), Is, flags, out.data_ptr(), _DT[out_dtype], workspace.data_ptr(), workspace.numel(),
+         _ptr(ids), _ptr(w), _stream(x))
+    if return_routing:
+        return out, ids, w
+    return out

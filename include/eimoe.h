@@ -1,0 +1,155 @@
+/* eimoe — MI355X (gfx950) fused-MoE expert path, C ABI.
+ *
+ * Drop-in boundary for EasyInfra's MoE expert plugin point
+ * (easyinfra/generation/modules/moe/config.py:4-15 get_moe_impl, the FusedMoE
+ * class of fused_moe.py:15-156) and its native grouped-GEMM op point
+ * (easyinfra/__init__.py:7-20, single_group_gemm_moe.py:53-91).
+ *
+ * Conventions
+ *  - Every pointer argument except the stream is a DEVICE pointer unless noted.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).  All work is
+ *    enqueued on it; no entry point synchronises the device or allocates memory.  The caller
+ *    owns every buffer, including the workspace.
+ *  - Return value: EIMOE_OK (0) or a negative EIMOE_ERR_* code; eimoe_last_error() then
+ *    returns a message (thread-local).  Arguments are validated on the host before any launch.
+ *  - dtype codes: EIMOE_F32, EIMOE_BF16, EIMOE_FP8 (OCP e4m3fn, one byte).
+ *  - Row/column-major: all matrices are row-major with the given leading dimension; expert
+ *    weights use nn.Linear layout [out_features, in_features] (K contiguous).
+ *  - Integer outputs (ids, counts, offsets, permutations) are deterministic and bit-exact.
+ */
+#ifndef EIMOE_H_
+#define EIMOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EIMOE_ABI_VERSION 1
+
+enum {
+  EIMOE_OK = 0,
+  EIMOE_ERR_NULL = -1,      /* a required pointer is NULL */
+  EIMOE_ERR_SHAPE = -2,     /* a size is out of the supported range */
+  EIMOE_ERR_ALIGN = -3,     /* a dimension is not a multiple of the required granule */
+  EIMOE_ERR_DTYPE = -4,     /* unsupported dtype code / combination */
+  EIMOE_ERR_WORKSPACE = -5, /* workspace smaller than eimoe_fused_moe_workspace_bytes() */
+  EIMOE_ERR_HIP = -6        /* the HIP runtime reported an error at launch */
+};
+
+enum { EIMOE_F32 = 0, EIMOE_BF16 = 1, EIMOE_FP8 = 2 };
+
+/* flags for eimoe_fused_moe */
+enum {
+  EIMOE_RENORMALIZE = 1, /* renormalise the top-k weights (norm_topk_prob) */
+  EIMOE_Y_F32 = 2        /* keep the per-assignment expert outputs in fp32 (default: output dtype) */
+};
+
+/* tile selector for the GEMM entry points (0 = automatic) */
+enum { EIMOE_TILE_AUTO = 0, EIMOE_TILE_256x256 = 1, EIMOE_TILE_128x128 = 2, EIMOE_TILE_32x128 = 3,
+       EIMOE_TILE_16x64 = 4 };
+
+#define EIMOE_MAX_TOPK 32
+#define EIMOE_MAX_EXPERTS 512
+#define EIMOE_MAX_SEGMENTS 1024
+
+int eimoe_abi_version(void);
+const char* eimoe_last_error(void);
+
+/* Router: softmax -> top-k -> optional renormalisation.
+ * Replaces Qwen3MoeSparseMoeBlock._routing (models/qwen3_moe/modeling_qwen3_moe.py:255-266).
+ * logits [T,E] fp32 -> topk_ids [T,k] int32 (descending logit, ties to the lower id),
+ * topk_weights [T,k] fp32.  1 <= k <= min(E, EIMOE_MAX_TOPK), E <= EIMOE_MAX_EXPERTS. */
+int eimoe_router_topk(const float* logits, int T, int E, int k, int renormalize, int32_t* topk_ids,
+                      float* topk_weights, void* stream);
+
+/* Align: per-expert counts, offsets and the stable expert-major permutation.
+ * Replaces _MoeBlock._all_expert_count_compute (generation/blocks/moe/base.py:343-364) and the
+ * sort/index steps of MoeAll2AllBlock.all2all_chunk_routing_compute (blocks/moe/moe_all2all.py:346-348).
+ * Only ids in [e_lo, e_lo+n_local) are kept (one GPU's EP share, blocks/moe/base.py:162-169, 187).
+ * Outputs: counts[n_local], offsets[n_local+1] (offsets[n_local] = rows kept),
+ * sorted_flat[T*k] (flat index t*k+slot per row), sorted_tok[T*k] (t per row),
+ * pos[T*k] (row of each flat index, -1 if not local).  Rows beyond offsets[n_local] are untouched.
+ * 1 <= n_local <= EIMOE_MAX_EXPERTS. */
+int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, int32_t* counts, int32_t* offsets,
+                int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream);
+
+/* Segment offsets from per-segment row counts (exclusive prefix sum, offsets[n_seg] = total).
+ * Replaces the block schedule of TritonExperts.forward_ep (fused_moe.py:413-439) for callers that
+ * pass pre-grouped rows (FusedMoE.forward_ep(hidden_states, expert_count), fused_moe.py:106-156). */
+int eimoe_counts_to_offsets(const int32_t* counts, int n_seg, int32_t* offsets, void* stream);
+
+/* Gather: xs[r,:] = x[rows[r],:] for r < min(*num_rows, max_rows).
+ * Replaces send_hidden_states = h[send_indices] (blocks/moe/moe_all2all.py:351).
+ * dtype EIMOE_F32 or EIMOE_BF16; H*elem_size must be a multiple of 16 bytes. */
+int eimoe_gather(const void* x, int dtype, int H, const int32_t* rows, const int32_t* num_rows, int max_rows,
+                 void* xs, void* stream);
+
+/* Grouped gate/up GEMM with SiLU*mul fused:  h[r,:] = silu(g) * u, [g|u] = a[row(r)] . W_gu[e]^T
+ * for r in segment s (rows [seg_offsets[s], seg_offsets[s+1])), e = s % e_mod.
+ * Replaces fused_moe.py:445-459 (first fused_moe_kernel launch + silu(g)*u).
+ * a: bf16, row r reads a[(a_rows ? a_rows[r] : r) * lda + :H] (a_rows gathers tokens directly).
+ * w_gate_up: [E_w, 2I, H] bf16 or fp8 (rows [0,I) gate, [I,2I) up, fused_moe.py:91-101);
+ * w_scale: fp8 only, [E_w, 2I] fp32 per-output-channel scales.  h: bf16 [max_rows, I].
+ * H % 64 == 0, I % 32 == 0.  max_rows bounds seg_offsets[n_seg]. */
+int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int lda, const void* w_gate_up, int w_dtype,
+                            const float* w_scale, int H, int I, const int32_t* seg_offsets, int n_seg, int e_mod,
+                            int max_rows, void* h, int tile, void* stream);
+
+/* Grouped down GEMM: y[r,:] = h[r,:] . W_d[e]^T (fused_moe.py:463-476).
+ * h: bf16 [max_rows, I]; w_down: [E_w, H, I] bf16 or fp8 (+ w_scale [E_w, H]).
+ * y: y_dtype (EIMOE_F32 / EIMOE_BF16) [k_split][max_rows, H]; with k_split > 1 each K-slice
+ * writes its own partial plane (summed by eimoe_combine), I/k_split % 64 == 0. */
+int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const float* w_scale, int H,
+                    const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows, void* y, int y_dtype,
+                    int k_split, int tile, void* stream);
+
+/* Plain grouped GEMM, the X_grouped_gemm_single(A, B_list, block_sizes) contract
+ * (single_group_gemm_moe.py:76-91): c[rows_s] = a[rows_s] . B[s % e_mod]^T with B packed as
+ * [E_w, N, K] (b_expert_stride elements apart).  a bf16; b bf16/fp8 (+b_scale [E_w,N]);
+ * c f32 or bf16 [max_rows, N].  K % 64 == 0, N % 64 == 0. */
+int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int lda, const void* b, int b_dtype,
+                       const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
+                       int n_seg, int e_mod, int max_rows, void* c, int c_dtype, int tile, void* stream);
+
+/* Weighted top-k combine: out[t,:] = sum_j w[t,j] * sum_s y[s][pos[t*k+j],:]  (+ shared_y[t,:]).
+ * Replaces _all2all_chunk_output_compute (blocks/moe/moe_all2all.py:291-307) and the shared-expert
+ * residual add (moe_all2all.py:535-537).  Slots with pos < 0 contribute nothing; a token with no
+ * local slot gets a zero row (or just shared_y).  fp32 accumulation, deterministic.
+ * y: y_dtype [n_split][*, H] planes split_stride elements apart; shared_y optional [T,H]. */
+int eimoe_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
+                  const float* topk_weights, int T, int k, int H, const void* shared_y, int shared_dtype, void* out,
+                  int out_dtype, void* stream);
+
+/* fp8 quantisation per row: scale[r] = max|x[r,:]|/448 (1 for a zero row), q = rne_e4m3fn(x/scale).
+ * Used for per-output-channel weight scales and per-token activation scales.  No reference
+ * counterpart (fused_moe.py:331-335 takes no scales). */
+int eimoe_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,
+                            void* stream);
+
+/* Workspace bytes for eimoe_fused_moe with these sizes and flags. */
+size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_local, int shared_inter,
+                                       int out_dtype, int flags);
+
+/* The whole layer: hidden_states, router logits and top_k in, combined output out.
+ * Composes router -> align -> gate/up+SiLU (gathering x rows directly) -> down -> combine
+ * (+ shared experts), i.e. MoeAll2AllBlock's stages at ep=1 (blocks/moe/moe_all2all.py:85-95)
+ * with FusedMoE.forward_ep (fused_moe.py:106-156) as the expert step.
+ *   x [T,H] bf16; logits [T,E] fp32; w_gate_up [n_local,2I,H], w_down [n_local,H,I] in w_dtype
+ *   (bf16 or fp8 with per-channel scales [n_local,2I] / [n_local,H]); experts e_lo..e_lo+n_local-1
+ *   of the router's E are resident (pass 0, E for a whole layer); shared experts optional
+ *   (shared_gate_up [2*Is,H], shared_down [H,Is] bf16, weight 1.0); out [T,H] in out_dtype.
+ * Optional outputs (may be NULL): topk_ids_out [T,k] int32, topk_w_out [T,k] fp32. */
+int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int E, int k, const void* w_gate_up,
+                    const void* w_down, int w_dtype, const float* w_gate_up_scale, const float* w_down_scale, int e_lo,
+                    int n_local, const void* shared_gate_up, const void* shared_down, int shared_inter, int flags,
+                    void* out, int out_dtype, void* workspace, size_t workspace_bytes, int32_t* topk_ids_out,
+                    float* topk_w_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EIMOE_H_ */

@@ -1,0 +1,298 @@
+"""CPU oracle for the fused-MoE expert path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker (or, in the bench, as the timed CPU baseline).  The product path
+(``easyinfra_amd``) never calls it; it fails loudly when its HIP library is
+missing.
+
+This is a restatement of EasyInfra's single-GPU (ep=1) MoE layer semantics,
+with every collective replaced by the identity it is at group size 1
+(easyinfra/generation/parallel/communicator.py:143-148, 168-172, 270-271):
+
+  route_topk     modeling_qwen3_moe.py:255-266 (softmax -> top-k -> renorm)
+  align          blocks/moe/base.py:343-364 (per-expert counts),
+                 moe_all2all.py:346-348 (sort, token index, slot), with the
+                 EP-local expert window of blocks/moe/base.py:162-169, 187
+  gather         moe_all2all.py:351
+  expert_mlp     modules/moe/base.py:39-42, native_moe.py:56-103,
+                 fused_moe.py:445-476 (gate/up -> silu(g)*u -> down)
+  combine        moe_all2all.py:291-307 (weighted index_add_)
+  shared_mlp     blocks/mlp.py:78-81 (+ modeling_deepseek_v3.py:213 sizing)
+  moe_forward    moe_all2all.py:85-95 stages composed (a14)
+
+Two deliberate, documented choices where the reference is not reproducible:
+  * Top-k ties: the reference's ``torch.topk`` tie order is implementation
+    defined.  The oracle selects by logit value (softmax is monotonic), ties to
+    the lower expert id.
+  * Sort stability: ``torch.sort(stable=False)`` (moe_all2all.py:346) promises
+    no order among equal experts.  The oracle pins the stable order
+    (expert, then flat index t*k+slot).
+
+fp8 helpers (weight per-output-channel absmax/448 scales, per-token dynamic
+activation scales, OCP e4m3fn with round-to-nearest-even as torch's CPU cast)
+have no counterpart in the reference (fused_moe.py:331-335 maps fp8 inputs to
+a bf16 compute type and takes no scales).
+
+Pinning: every function here is checked in tests/test_oracle.py against an
+independent formulation (brute-force loops on tiny shapes, a dense
+all-experts-masked formulation, float64 closed forms, invariants), not by
+re-typing the formula.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+FP8_MAX = 448.0
+
+
+# --------------------------------------------------------------------------- router
+def route_topk(logits: torch.Tensor, k: int, renormalize: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+    """modeling_qwen3_moe.py:255-266.
+
+    probs = softmax(logits, fp32); ids = top-k (canonical: by logit, ties -> lower id);
+    w = probs[ids], renormalised over the k picks when ``renormalize``.
+    Returns (ids int32 [T,k], w fp32 [T,k]).  Weights stay fp32 (the reference casts
+    them to the activation dtype before the combine; the oracle keeps fp32).
+    """
+    logits = torch.as_tensor(logits).to(torch.float32)
+    probs = torch.softmax(logits, dim=-1, dtype=torch.float32)
+    ids = torch.sort(-logits, dim=-1, stable=True).indices[:, :k]
+    w = probs.gather(1, ids)
+    if renormalize:
+        w = w / w.sum(dim=-1, keepdim=True)
+    return ids.to(torch.int32), w
+
+
+# --------------------------------------------------------------------------- align
+def align(ids: np.ndarray, n_local: int, e_lo: int = 0):
+    """Counts, offsets, stable expert-major permutation and its inverse.
+
+    blocks/moe/base.py:343-364: counts = zeros(E).scatter_add_(ids, 1), restricted to
+    the local window [e_lo, e_lo+n_local) (base.py:187).  moe_all2all.py:346-348:
+    sorted flat positions, token = flat // k, slot = flat % k.
+
+    Returns dict of int32 numpy arrays: counts[n_local], offsets[n_local+1],
+    sorted_flat[A], sorted_tok[A], pos[T*k] (row of each flat slot, -1 if not local).
+    """
+    ids = np.asarray(ids)
+    T, k = ids.shape
+    flat = ids.reshape(-1).astype(np.int64) - e_lo
+    local = (flat >= 0) & (flat < n_local)
+    counts = np.bincount(flat[local], minlength=n_local).astype(np.int64)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    idx = np.nonzero(local)[0]
+    order = idx[np.argsort(flat[idx], kind="stable")]
+    pos = np.full(T * k, -1, dtype=np.int64)
+    pos[order] = np.arange(order.size)
+    return {
+        "counts": counts.astype(np.int32),
+        "offsets": offsets.astype(np.int32),
+        "sorted_flat": order.astype(np.int32),
+        "sorted_tok": (order // k).astype(np.int32),
+        "sorted_slot": (order % k).astype(np.int32),
+        "pos": pos.astype(np.int32),
+    }
+
+
+def gather(x: torch.Tensor, sorted_tok) -> torch.Tensor:
+    """moe_all2all.py:351: send_hidden_states = h[send_indices]."""
+    return x[torch.as_tensor(np.asarray(sorted_tok), dtype=torch.long)]
+
+
+# --------------------------------------------------------------------------- experts
+def silu(x: torch.Tensor) -> torch.Tensor:
+    """activation/base_activation.py:8-11 (torch.nn.SiLU): x * sigmoid(x)."""
+    return x * torch.sigmoid(x)
+
+
+def _round_bf16(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16).to(torch.float32)
+
+
+def expert_mlp(xs: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
+               round_h_bf16: bool = False) -> torch.Tensor:
+    """One expert: modules/moe/base.py:39-42 / fused_moe.py:445-476, fp32 math.
+
+    gu = xs @ W_gu^T (rows [0,I) gate, [I,2I) up); h = silu(g) * u; y = h @ W_d^T.
+    ``round_h_bf16`` rounds h to bf16 before the down projection, the storage
+    precision of the GPU path's intermediate (used for tighter checks only).
+    """
+    I = w_down.shape[1]
+    gu = F.linear(xs.float(), w_gate_up.float())
+    h = silu(gu[:, :I]) * gu[:, I:]
+    if round_h_bf16:
+        h = _round_bf16(h)
+    return F.linear(h, w_down.float())
+
+
+def shared_mlp(x: torch.Tensor, shared_gate_up: torch.Tensor, shared_down: torch.Tensor,
+               round_h_bf16: bool = False) -> torch.Tensor:
+    """blocks/mlp.py:78-81: a dense SwiGLU MLP, weight 1.0, added to the layer output."""
+    return expert_mlp(x, shared_gate_up, shared_down, round_h_bf16)
+
+
+def moe_forward(x: torch.Tensor, logits: torch.Tensor, k: int, w_gate_up: torch.Tensor,
+                w_down: torch.Tensor, renormalize: bool = True,
+                shared_gate_up: Optional[torch.Tensor] = None, shared_down: Optional[torch.Tensor] = None,
+                expert_range: Optional[Tuple[int, int]] = None, round_h_bf16: bool = False,
+                token_subset: Optional[torch.Tensor] = None, return_parts: bool = False):
+    """The layer at ep=1 (moe_all2all.py:85-95): route -> align -> gather -> experts -> combine.
+
+    ``expert_range=(lo,hi)`` keeps only assignments to experts [lo,hi) (one GPU's EP
+    share, blocks/moe/base.py:162-169); ``w_gate_up/w_down`` then hold those experts
+    only.  Tokens with no local expert produce zero rows.  ``token_subset`` evaluates
+    only the given token rows (the layer is row-independent given the logits).
+    Returns fp32 [T or |subset|, H].
+    """
+    x = torch.as_tensor(x)
+    logits = torch.as_tensor(logits).float()
+    if token_subset is not None:
+        token_subset = torch.as_tensor(token_subset, dtype=torch.long)
+        x, logits = x[token_subset], logits[token_subset]
+    T, H = x.shape
+    ids, w = route_topk(logits, k, renormalize)
+    lo, hi = expert_range if expert_range is not None else (0, w_gate_up.shape[0])
+    al = align(ids.numpy(), hi - lo, lo)
+    out = torch.zeros(T, H, dtype=torch.float32)
+    xs = gather(x, al["sorted_tok"]).float()
+    tok = torch.as_tensor(al["sorted_tok"], dtype=torch.long)
+    slot = torch.as_tensor(al["sorted_slot"], dtype=torch.long)
+    w_sorted = w[tok, slot]                                   # moe_all2all.py:193
+    ys = torch.empty(xs.shape[0], H, dtype=torch.float32)
+    off = al["offsets"]
+    for e in range(hi - lo):
+        a, b = int(off[e]), int(off[e + 1])
+        if b > a:
+            ys[a:b] = expert_mlp(xs[a:b], w_gate_up[e], w_down[e], round_h_bf16)
+    out.index_add_(0, tok, ys * w_sorted[:, None])            # moe_all2all.py:302-304
+    if shared_gate_up is not None:
+        out += shared_mlp(x.float(), shared_gate_up, shared_down, round_h_bf16)
+    if return_parts:
+        return out, {"ids": ids, "w": w, "align": al, "ys": ys}
+    return out
+
+
+def moe_forward_dense(x, logits, k, w_gate_up, w_down, renormalize=True, shared_gate_up=None,
+                      shared_down=None, expert_range=None) -> torch.Tensor:
+    """Independent formulation used only to pin ``moe_forward``: every token through
+    every local expert, combined with a dense [T,E] gate matrix (zeros off the top-k),
+    float64 throughout.  No sort, no gather, no index_add_."""
+    x = torch.as_tensor(x).double()
+    logits = torch.as_tensor(logits).double()
+    T, E = logits.shape
+    lo, hi = expert_range if expert_range is not None else (0, w_gate_up.shape[0])
+    p = torch.softmax(logits, dim=-1)
+    gate = torch.zeros(T, E, dtype=torch.float64)
+    for t in range(T):
+        order = sorted(range(E), key=lambda e: (-float(logits[t, e]), e))[:k]
+        sel = torch.tensor(order)
+        wt = p[t, sel]
+        if renormalize:
+            wt = wt / wt.sum()
+        gate[t, sel] = wt
+    I = w_down.shape[2]
+    out = torch.zeros(T, x.shape[1], dtype=torch.float64)
+    for e in range(hi - lo):
+        gu = x @ w_gate_up[e].double().T
+        h = gu[:, :I] * torch.sigmoid(gu[:, :I]) * gu[:, I:]
+        out += gate[:, lo + e:lo + e + 1] * (h @ w_down[e].double().T)
+    if shared_gate_up is not None:
+        Is = shared_down.shape[1]
+        gu = x @ shared_gate_up.double().T
+        out += (gu[:, :Is] * torch.sigmoid(gu[:, :Is]) * gu[:, Is:]) @ shared_down.double().T
+    return out
+
+
+# --------------------------------------------------------------------------- fp8
+def quantize_rows_fp8(t: torch.Tensor):
+    """Per-row absmax/448 scale and OCP e4m3fn values (torch CPU cast, RNE).
+
+    Used for weights (one scale per output channel = per row of [E*N, K]) and for
+    activations (one scale per token).  Returns (q float8_e4m3fn, scale fp32 [rows]).
+    A zero row gets scale 1 (its values quantise to 0 either way).
+    """
+    t32 = t.float()
+    amax = t32.abs().amax(dim=-1)
+    scale = amax / FP8_MAX
+    scale = torch.where(amax > 0, scale, torch.ones_like(scale))
+    q = (t32 / scale.unsqueeze(-1)).to(torch.float8_e4m3fn)
+    return q, scale
+
+
+def quantize_weights_fp8(w: torch.Tensor):
+    """[E,N,K] -> (q [E,N,K] e4m3fn, scale [E,N] fp32): per-output-channel scales."""
+    E, N, K = w.shape
+    q, s = quantize_rows_fp8(w.reshape(E * N, K))
+    return q.view(E, N, K), s.view(E, N)
+
+
+def expert_mlp_fp8(xs, wq_gu, s_gu, wq_d, s_d, mode: str = "w8a8") -> torch.Tensor:
+    """One expert with fp8 weights.
+
+    w8a16: y = ((x @ Wq_gu^T) * s_gu -> silu*mul) @ Wq_d^T * s_d, activations in
+           bf16-exact fp32.
+    w8a8:  activations dynamically quantised per token before each GEMM:
+           gu = (xq @ Wq^T) * s_x[:,None] * s_gu[None,:]; h likewise with its row scale.
+    """
+    I = wq_d.shape[1]
+    wgu = wq_gu.float()
+    wd = wq_d.float()
+    if mode == "w8a8":
+        xq, sx = quantize_rows_fp8(xs)
+        gu = (xq.float() @ wgu.T) * sx[:, None] * s_gu[None, :]
+    else:
+        gu = (xs.float() @ wgu.T) * s_gu[None, :]
+    h = silu(gu[:, :I]) * gu[:, I:]
+    if mode == "w8a8":
+        hq, sh = quantize_rows_fp8(h)
+        return (hq.float() @ wd.T) * sh[:, None] * s_d[None, :]
+    h = _round_bf16(h)
+    return (h @ wd.T) * s_d[None, :]
+
+
+def moe_forward_fp8(x, logits, k, wq_gu, s_gu, wq_d, s_d, renormalize=True, mode="w8a8",
+                    expert_range=None, token_subset=None) -> torch.Tensor:
+    """moe_forward with fp8 expert weights (see expert_mlp_fp8)."""
+    x = torch.as_tensor(x)
+    logits = torch.as_tensor(logits).float()
+    if token_subset is not None:
+        token_subset = torch.as_tensor(token_subset, dtype=torch.long)
+        x, logits = x[token_subset], logits[token_subset]
+    T, H = x.shape
+    ids, w = route_topk(logits, k, renormalize)
+    lo, hi = expert_range if expert_range is not None else (0, wq_gu.shape[0])
+    al = align(ids.numpy(), hi - lo, lo)
+    tok = torch.as_tensor(al["sorted_tok"], dtype=torch.long)
+    slot = torch.as_tensor(al["sorted_slot"], dtype=torch.long)
+    xs = x[tok].float()
+    ys = torch.empty(xs.shape[0], H, dtype=torch.float32)
+    off = al["offsets"]
+    for e in range(hi - lo):
+        a, b = int(off[e]), int(off[e + 1])
+        if b > a:
+            ys[a:b] = expert_mlp_fp8(xs[a:b], wq_gu[e], s_gu[e], wq_d[e], s_d[e], mode)
+    out = torch.zeros(T, H, dtype=torch.float32)
+    out.index_add_(0, tok, ys * w[tok, slot][:, None])
+    return out
+
+
+# --------------------------------------------------------------------------- grouped GEMM
+def grouped_gemm(a: torch.Tensor, b_list, block_sizes) -> torch.Tensor:
+    """single_group_gemm_moe.py:76-91 contract: out[rows_i] = A[rows_i] @ B_i^T over
+    contiguous row blocks, B_i in nn.Linear layout [N,K]; fp32 result."""
+    outs, r = [], 0
+    for b, n in zip(b_list, block_sizes):
+        outs.append(F.linear(a[r:r + n].float(), b.float()))
+        r += n
+    return torch.cat(outs, 0) if outs else a.new_zeros(0, b_list[0].shape[0], dtype=torch.float32)
+
+
+def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
+    a = a.double()
+    b = b.double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))

@@ -1,0 +1,237 @@
+"""Per-kernel parity on the GPU: each C-ABI entry point against the CPU oracle.
+
+Integer outputs (router ids, counts, offsets, permutations, fp8 bytes) must be
+bit-exact.  GEMM outputs are compared with the oracle's fp32 math on the same
+bf16 inputs; the tolerance covers bf16 storage of the result (2^-8 relative) and
+fp32 accumulation-order differences.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from easyinfra_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def cpu(t):
+    return t.detach().cpu()
+
+
+def _distinct_ids(T, E, k, gen, weights=None):
+    if weights is None:
+        return torch.rand(T, E, generator=gen).argsort(dim=1)[:, :k].to(torch.int32)
+    return torch.multinomial(weights.expand(T, E), k, replacement=False, generator=gen).to(torch.int32)
+
+
+# --------------------------------------------------------------------------- router
+@pytest.mark.parametrize("T,E,k,renorm", [
+    (1, 8, 2, True), (37, 8, 2, True), (512, 8, 2, True), (257, 64, 6, False), (100, 128, 8, True),
+    (64, 16, 4, True), (33, 32, 3, False), (10, 256, 8, True), (5, 512, 32, True), (3, 5, 5, True),
+    (300, 100, 1, False),
+])
+def test_router_topk_matches_oracle(dev, T, E, k, renorm):
+    g = torch.Generator().manual_seed(T * 1000 + E)
+    logits = torch.randn(T, E, generator=g) * 2.0
+    ids, w = ops.router_topk(logits.to(dev), k, renorm)
+    rid, rw = oracle.route_topk(logits, k, renorm)
+    assert torch.equal(cpu(ids), rid)
+    torch.testing.assert_close(cpu(w), rw, rtol=3e-6, atol=1e-7)
+
+
+def test_router_ties_go_to_lower_expert(dev):
+    logits = torch.tensor([[1., 1., 1., 1., 0., 0., 0., 0.],
+                           [0., 2., 2., 0., 2., 0., 0., 0.],
+                           [-1., -1., -1., -1., -1., -1., -1., -1.],
+                           [0., 0., 0., 0., 0., 0., 3., 3.]])
+    ids, w = ops.router_topk(logits.to(dev), 3, True)
+    assert cpu(ids).tolist() == [[0, 1, 2], [1, 2, 4], [0, 1, 2], [6, 7, 0]]
+    rid, rw = oracle.route_topk(logits, 3, True)
+    assert torch.equal(cpu(ids), rid)
+    torch.testing.assert_close(cpu(w), rw, rtol=3e-6, atol=1e-7)
+
+
+def test_router_empty(dev):
+    ids, w = ops.router_topk(torch.empty(0, 8, device=dev), 2)
+    assert ids.shape == (0, 2) and w.shape == (0, 2)
+
+
+# --------------------------------------------------------------------------- align
+@pytest.mark.parametrize("T,k,E,e_lo,n_loc,skew", [
+    (1, 2, 8, 0, 8, False), (512, 2, 8, 0, 8, False), (8192, 2, 8, 0, 8, False), (4096, 6, 64, 0, 64, True),
+    (2048, 8, 128, 0, 32, True), (2048, 8, 128, 32, 32, False), (1000, 8, 128, 96, 32, False), (7, 3, 5, 1, 3, False),
+    (3, 1, 1, 0, 1, False), (16384, 8, 512, 0, 512, False),
+])
+def test_align_bit_exact(dev, T, k, E, e_lo, n_loc, skew):
+    g = torch.Generator().manual_seed(T + 7 * E + e_lo)
+    wts = (1.0 / torch.arange(1, E + 1, dtype=torch.float32) ** 1.2) if skew else None
+    ids = _distinct_ids(T, E, k, g, wts)
+    got = ops.align(ids.to(dev), n_loc, e_lo)
+    ref = oracle.align(ids.numpy(), n_loc, e_lo)
+    A = int(ref["offsets"][-1])
+    assert np.array_equal(cpu(got["counts"]).numpy(), ref["counts"])
+    assert np.array_equal(cpu(got["offsets"]).numpy(), ref["offsets"])
+    assert np.array_equal(cpu(got["sorted_flat"])[:A].numpy(), ref["sorted_flat"])
+    assert np.array_equal(cpu(got["sorted_tok"])[:A].numpy(), ref["sorted_tok"])
+    assert np.array_equal(cpu(got["pos"]).numpy(), ref["pos"])
+
+
+def test_align_all_to_one_expert_and_repeats(dev):
+    ids = torch.full((300, 4), 3, dtype=torch.int32)
+    ids[::7, 1] = 0
+    got = ops.align(ids.to(dev), 5, 0)
+    ref = oracle.align(ids.numpy(), 5, 0)
+    A = int(ref["offsets"][-1])
+    for key in ("counts", "offsets", "pos"):
+        assert np.array_equal(cpu(got[key]).numpy(), ref[key]), key
+    assert np.array_equal(cpu(got["sorted_flat"])[:A].numpy(), ref["sorted_flat"])
+
+
+def test_align_out_of_window_ids_dropped(dev):
+    ids = torch.tensor([[0, 9], [5, 2], [7, 8]], dtype=torch.int32)
+    got = ops.align(ids.to(dev), 4, 2)
+    ref = oracle.align(ids.numpy(), 4, 2)
+    # window [2,6): id 2 -> local 0 (flat 3), id 5 -> local 3 (flat 2)
+    assert cpu(got["counts"]).tolist() == [1, 0, 0, 1] == ref["counts"].tolist()
+    assert cpu(got["pos"]).tolist() == [-1, -1, 1, 0, -1, -1]
+
+
+# --------------------------------------------------------------------------- gather / combine
+def test_gather_rows(dev):
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(50, 256, generator=g).to(torch.bfloat16)
+    rows = torch.randint(0, 50, (70,), generator=g, dtype=torch.int32)
+    n = torch.tensor([61], dtype=torch.int32)
+    xs = ops.gather(x.to(dev), rows.to(dev), n.to(dev), 70)
+    assert torch.equal(cpu(xs)[:61], x[rows[:61].long()])
+
+
+@pytest.mark.parametrize("y_dtype,out_dtype,n_split", [(torch.float32, torch.float32, 1), (torch.bfloat16, torch.bfloat16, 1),
+                                                        (torch.float32, torch.bfloat16, 3)])
+def test_combine_matches_index_add(dev, y_dtype, out_dtype, n_split):
+    g = torch.Generator().manual_seed(11)
+    T, k, E, H = 97, 3, 6, 128
+    ids = _distinct_ids(T, E, k, g)
+    al = oracle.align(ids.numpy(), 4, 1)           # experts 1..4 local: some slots dropped
+    A = int(al["offsets"][-1])
+    w = torch.rand(T, k, generator=g)
+    y = torch.randn(n_split, A, H, generator=g).to(y_dtype)
+    sh = torch.randn(T, H, generator=g)
+    got = ops.combine(y.to(dev), torch.as_tensor(al["pos"]).to(dev), w.to(dev), shared_y=sh.to(dev),
+                      out_dtype=out_dtype)
+    tok = torch.as_tensor(al["sorted_tok"]).long()
+    slot = torch.as_tensor(al["sorted_slot"]).long()
+    ref = torch.zeros(T, H)
+    ref.index_add_(0, tok, y.float().sum(0) * w[tok, slot][:, None])
+    ref += sh
+    tol = 1e-5 if out_dtype == torch.float32 else 8e-3
+    torch.testing.assert_close(cpu(got).float(), ref, rtol=tol, atol=tol)
+
+
+# --------------------------------------------------------------------------- GEMMs
+def _segments(counts):
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    return off, torch.as_tensor(off)
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("counts", [[0, 5, 300, 1, 64], [17], [0, 0, 3]])
+def test_gate_up_silu(dev, tile, counts):
+    g = torch.Generator().manual_seed(sum(counts) + tile)
+    H, I = 256, 256
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 40
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, T, (max(rows, 1),), generator=g, dtype=torch.int32)
+    w = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16)
+    h = ops.gemm_gate_up_silu(x.to(dev), w.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev), tile=tile)
+    h = cpu(h).float()
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        xs = x[a_rows[a:b].long()].float()
+        gu = xs @ w[e].float().T
+        ref = oracle.silu(gu[:, :I]) * gu[:, I:]
+        torch.testing.assert_close(h[a:b], ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 4)])
+def test_down_gemm(dev, tile, k_split):
+    g = torch.Generator().manual_seed(31 + tile * 7 + k_split)
+    H, I = 256, 512
+    counts = [3, 0, 257, 40]
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    h = torch.randn(rows, I, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16)
+    y = ops.gemm_down(h.to(dev), w.to(dev), off_t.to(dev), rows, out_dtype=torch.float32, k_split=k_split, tile=tile)
+    y = cpu(y).sum(0)
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        ref = h[a:b].float() @ w[e].float().T
+        torch.testing.assert_close(y[a:b], ref, rtol=1e-4, atol=1e-4)
+
+
+def test_grouped_gemm_single_contract(dev):
+    g = torch.Generator().manual_seed(3)
+    K, N = 192, 320
+    blocks = [10, 0, 33, 128]
+    a = torch.randn(sum(blocks), K, generator=g).to(torch.bfloat16)
+    b = (torch.randn(len(blocks), N, K, generator=g) * 0.1).to(torch.bfloat16)
+    off, off_t = _segments(blocks)
+    c = ops.grouped_gemm(a.to(dev), b.to(dev), off_t.to(dev), sum(blocks), out_dtype=torch.float32, tile=4)
+    ref = oracle.grouped_gemm(a, list(b), blocks)
+    torch.testing.assert_close(cpu(c), ref, rtol=1e-4, atol=1e-4)
+
+
+def test_gemm_rejects_bad_shapes(dev):
+    from easyinfra_amd._lib import EimoeError
+    a = torch.zeros(4, 100, dtype=torch.bfloat16, device=dev)
+    w = torch.zeros(1, 64, 100, dtype=torch.bfloat16, device=dev)
+    off = torch.tensor([0, 4], dtype=torch.int32, device=dev)
+    with pytest.raises(EimoeError):
+        ops.gemm_gate_up_silu(a, w, off, 4)
+
+
+# --------------------------------------------------------------------------- fp8
+@pytest.mark.parametrize("shape,dtype", [((7, 1000), torch.float32), ((64, 4096), torch.bfloat16),
+                                         ((3, 5), torch.float32), ((2, 16, 96), torch.bfloat16)])
+def test_quantize_rows_fp8_bit_exact(dev, shape, dtype):
+    g = torch.Generator().manual_seed(shape[0])
+    x = (torch.randn(*shape, generator=g) * 0.3).to(dtype)
+    x.view(-1, shape[-1])[0, :] = 0.0                      # an all-zero row -> scale 1
+    q, s = ops.quantize_rows_fp8(x.to(dev))
+    rq, rs = oracle.quantize_rows_fp8(x.reshape(-1, shape[-1]))
+    assert torch.equal(cpu(s).reshape(-1), rs)
+    assert torch.equal(cpu(q).reshape(-1, shape[-1]).view(torch.uint8), rq.view(torch.uint8))
+
+
+@pytest.mark.parametrize("tile", [2, 4])
+def test_fp8_weight_gemms(dev, tile):
+    g = torch.Generator().manual_seed(tile)
+    H, I, counts = 256, 256, [20, 0, 70]
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    x = torch.randn(rows, H, generator=g).to(torch.bfloat16)
+    wgu = torch.randn(E, 2 * I, H, generator=g) * 0.02
+    wd = torch.randn(E, H, I, generator=g) * 0.02
+    qgu, sgu = oracle.quantize_weights_fp8(wgu)
+    qd, sd = oracle.quantize_weights_fp8(wd)
+    h = ops.gemm_gate_up_silu(x.to(dev), qgu.to(dev), off_t.to(dev), rows, w_scale=sgu.to(dev), tile=tile)
+    y = ops.gemm_down(h, qd.to(dev), off_t.to(dev), rows, w_scale=sd.to(dev), tile=tile)
+    h, y = cpu(h).float(), cpu(y)[0]
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        gu = (x[a:b].float() @ qgu[e].float().T) * sgu[e]
+        href = oracle.silu(gu[:, :I]) * gu[:, I:]
+        torch.testing.assert_close(h[a:b], href, rtol=1e-2, atol=1e-2)
+        yref = (h[a:b] @ qd[e].float().T) * sd[e]
+        torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
