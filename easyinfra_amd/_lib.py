@@ -30,11 +30,12 @@ SIGNATURES = {
                             c_void_p, c_void_p]),
     "eimoe_counts_to_offsets": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "eimoe_gather": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
-    "eimoe_gemm_gate_up_silu": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_int,
+    "eimoe_gemm_gate_up_silu": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_int, c_int,
                                         c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p]),
     "eimoe_gemm_down": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_int, c_int,
                                 c_void_p, c_int, c_int, c_int, c_void_p]),
-    "eimoe_grouped_gemm": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_longlong, c_int, c_int,
+    "eimoe_grouped_gemm": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_longlong, c_int,
+                                   c_int,
                                    c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_int, c_void_p]),
     "eimoe_combine": (c_int, [c_void_p, c_int, c_int, c_longlong, c_void_p, c_void_p, c_int, c_int, c_int,
                               c_void_p, c_int, c_void_p, c_int, c_void_p]),

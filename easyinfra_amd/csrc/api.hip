@@ -111,9 +111,9 @@ __global__ void dense_segment_kernel(int32_t* off, int T) {
   }
 }
 
-int run_gate_up(const void* a, const int32_t* a_rows, int lda, const void* w, int w_dtype, const float* w_scale,
-                int H, int I, const int32_t* seg, int n_seg, int e_mod, int max_rows, void* h, int tile,
-                hipStream_t s) {
+int run_gate_up(const void* a, const int32_t* a_rows, long long a_nrows, int lda, const void* w, int w_dtype,
+                const float* w_scale, int H, int I, const int32_t* seg, int n_seg, int e_mod, int max_rows, void* h,
+                int tile, hipStream_t s) {
   GemmArgs p{};
   p.a = a;
   p.a_rows = a_rows;
@@ -134,6 +134,7 @@ int run_gate_up(const void* a, const int32_t* a_rows, int lda, const void* w, in
   p.c_split_stride = 0;
   p.k_split = 1;
   p.max_rows = max_rows;
+  p.a_rows_cap = a_rows ? a_nrows : max_rows;
   return hip_check(launch_grouped_gemm(p, kEpiSiluBF16, w_dtype == EIMOE_FP8, max_rows, tile, s), "gate_up gemm");
 }
 
@@ -159,6 +160,7 @@ int run_down(const void* h, int I, const void* w, int w_dtype, const float* w_sc
   p.c_split_stride = static_cast<long long>(max_rows) * H;
   p.k_split = k_split;
   p.max_rows = max_rows;
+  p.a_rows_cap = max_rows;
   const int epi = y_dtype == EIMOE_F32 ? kEpiStoreF32 : kEpiStoreBF16;
   return hip_check(launch_grouped_gemm(p, epi, w_dtype == EIMOE_FP8, max_rows, tile, s), "down gemm");
 }
@@ -229,7 +231,7 @@ int eimoe_gather(const void* x, int dtype, int H, const int32_t* rows, const int
   return hip_check(launch_gather_rows(x, row_bytes, rows, num_rows, max_rows, xs, S(stream)), "gather");
 }
 
-int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int lda, const void* w_gate_up, int w_dtype,
+int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* w_gate_up, int w_dtype,
                             const float* w_scale, int H, int I, const int32_t* seg_offsets, int n_seg, int e_mod,
                             int max_rows, void* h, int tile, void* stream) {
   int rc = check_gemm_common(max_rows, n_seg, e_mod);
@@ -238,6 +240,14 @@ int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int lda, const
   if (H < 64 || H % 64) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 64", H);
   if (I < 32 || I % 32) return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 32", I);
   if (lda < H) return fail(EIMOE_ERR_SHAPE, "lda=%d < H=%d", lda, H);
+  if (a_rows && a_nrows < 1) return fail(EIMOE_ERR_SHAPE, "a_nrows=%d < 1 with a row map", a_nrows);
+  if (!a_rows) a_nrows = max_rows;
+  if (static_cast<long long>(a_nrows) * lda * 2 > 0x7fffffffll)
+    return fail(EIMOE_ERR_SHAPE, "A buffer (%d rows x %d) exceeds 2 GiB", a_nrows, lda);
+  if (static_cast<long long>(e_mod) * 2 * I * H * (w_dtype == EIMOE_FP8 ? 1 : 2) < 0)
+    return fail(EIMOE_ERR_SHAPE, "weight size overflows");
+  if (2ll * I * H * (w_dtype == EIMOE_FP8 ? 1 : 2) > 0x7fffffffll)
+    return fail(EIMOE_ERR_SHAPE, "one expert's gate/up weights exceed 2 GiB");
   if (lda % 8) return fail(EIMOE_ERR_ALIGN, "lda=%d must be a multiple of 8", lda);
   if ((rc = check_tile(tile, kEpiSiluBF16, I))) return rc;
   if (max_rows == 0) return EIMOE_OK;
@@ -246,8 +256,8 @@ int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int lda, const
   REQUIRE_PTR(seg_offsets);
   REQUIRE_PTR(h);
   if (w_dtype == EIMOE_FP8) REQUIRE_PTR(w_scale);
-  return run_gate_up(a, a_rows, lda, w_gate_up, w_dtype, w_scale, H, I, seg_offsets, n_seg, e_mod, max_rows, h, tile,
-                     S(stream));
+  return run_gate_up(a, a_rows, a_nrows, lda, w_gate_up, w_dtype, w_scale, H, I, seg_offsets, n_seg, e_mod, max_rows,
+                     h, tile, S(stream));
 }
 
 int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const float* w_scale, int H,
@@ -262,6 +272,10 @@ int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const
   if (I < 64 || I % (64 * k_split))
     return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 64*k_split=%d", I, 64 * k_split);
   if ((rc = check_tile(tile, kEpiStoreF32, H))) return rc;
+  if (static_cast<long long>(max_rows) * I * 2 > 0x7fffffffll)
+    return fail(EIMOE_ERR_SHAPE, "h (%d rows x %d) exceeds 2 GiB", max_rows, I);
+  if (static_cast<long long>(H) * I * (w_dtype == EIMOE_FP8 ? 1 : 2) > 0x7fffffffll)
+    return fail(EIMOE_ERR_SHAPE, "one expert's down weights exceed 2 GiB");
   if (max_rows == 0) return EIMOE_OK;
   REQUIRE_PTR(h);
   REQUIRE_PTR(w_down);
@@ -272,7 +286,7 @@ int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const
                   S(stream));
 }
 
-int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int lda, const void* b, int b_dtype,
+int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* b, int b_dtype,
                        const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
                        int n_seg, int e_mod, int max_rows, void* c, int c_dtype, int tile, void* stream) {
   int rc = check_gemm_common(max_rows, n_seg, e_mod);
@@ -284,6 +298,12 @@ int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int lda, const void
   if (lda < K || lda % 8) return fail(EIMOE_ERR_SHAPE, "lda=%d must be >= K=%d and a multiple of 8", lda, K);
   if (b_expert_stride < static_cast<long long>(N) * K)
     return fail(EIMOE_ERR_SHAPE, "b_expert_stride=%lld < N*K", b_expert_stride);
+  if (b_expert_stride * (b_dtype == EIMOE_FP8 ? 1 : 2) > 0x7fffffffll)
+    return fail(EIMOE_ERR_SHAPE, "one expert's weights exceed 2 GiB");
+  if (a_rows && a_nrows < 1) return fail(EIMOE_ERR_SHAPE, "a_nrows=%d < 1 with a row map", a_nrows);
+  if (!a_rows) a_nrows = max_rows;
+  if (static_cast<long long>(a_nrows) * lda * 2 > 0x7fffffffll)
+    return fail(EIMOE_ERR_SHAPE, "A buffer (%d rows x %d) exceeds 2 GiB", a_nrows, lda);
   if ((rc = check_tile(tile, kEpiStoreF32, N))) return rc;
   if (max_rows == 0) return EIMOE_OK;
   REQUIRE_PTR(a);
@@ -309,6 +329,7 @@ int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int lda, const void
   p.ldc = N;
   p.k_split = 1;
   p.max_rows = max_rows;
+  p.a_rows_cap = a_nrows;
   const int epi = c_dtype == EIMOE_F32 ? kEpiStoreF32 : kEpiStoreBF16;
   return hip_check(launch_grouped_gemm(p, epi, b_dtype == EIMOE_FP8, max_rows, tile, S(stream)), "grouped_gemm");
 }
@@ -406,7 +427,7 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos, s),
                       "align")))
     return rc;
-  if ((rc = run_gate_up(x, sorted_tok, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local, A,
+  if ((rc = run_gate_up(x, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local, A,
                         at(L.h), EIMOE_TILE_AUTO, s)))
     return rc;
   if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y), L.y_dtype,
@@ -417,7 +438,7 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
     int32_t* sh_off = static_cast<int32_t*>(at(L.sh_off));
     hipLaunchKernelGGL(dense_segment_kernel, dim3(1), dim3(64), 0, s, sh_off, T);
     if ((rc = hip_check(hipGetLastError(), "shared offsets"))) return rc;
-    if ((rc = run_gate_up(x, nullptr, H, shared_gate_up, EIMOE_BF16, nullptr, H, shared_inter, sh_off, 1, 1, T,
+    if ((rc = run_gate_up(x, nullptr, T, H, shared_gate_up, EIMOE_BF16, nullptr, H, shared_inter, sh_off, 1, 1, T,
                           at(L.sh_h), EIMOE_TILE_AUTO, s)))
       return rc;
     if ((rc = run_down(at(L.sh_h), shared_inter, shared_down, EIMOE_BF16, nullptr, H, sh_off, 1, 1, T, at(L.sh_y),

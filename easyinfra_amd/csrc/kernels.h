@@ -32,6 +32,7 @@ struct GemmArgs {
   long long c_split_stride;  // elements between split-K partial outputs
   int k_split;
   int max_rows;              // rows of A (non-gathered) / of C; segment bounds are clamped to it
+  long long a_rows_cap;      // rows in the A buffer (bounds the buffer resource)
 };
 
 // Tile shape selector; the launcher maps it to a kernel instantiation.

@@ -106,7 +106,8 @@ def gemm_gate_up_silu(a: torch.Tensor, w_gate_up: torch.Tensor, seg_offsets: tor
     if w_scale is not None:
         _req(w_scale, "w_scale", torch.float32)
     h = torch.empty(max_rows, I, dtype=torch.bfloat16, device=a.device)
-    call("eimoe_gemm_gate_up_silu", a.data_ptr(), _ptr(a_rows), a.stride(0), w_gate_up.data_ptr(), _dt(w_gate_up),
+    call("eimoe_gemm_gate_up_silu", a.data_ptr(), _ptr(a_rows), a.shape[0], a.stride(0), w_gate_up.data_ptr(),
+         _dt(w_gate_up),
          _ptr(w_scale), H, I, seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, h.data_ptr(),
          tile, _stream(a))
     return h
@@ -138,7 +139,8 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg_offsets: torch.Tensor, ma
     _req(seg_offsets, "seg_offsets", torch.int32, 1)
     E, N, K = b.shape
     c = torch.empty(max_rows, N, dtype=out_dtype, device=a.device)
-    call("eimoe_grouped_gemm", a.data_ptr(), _ptr(a_rows), a.stride(0), b.data_ptr(), _dt(b), _ptr(b_scale),
+    call("eimoe_grouped_gemm", a.data_ptr(), _ptr(a_rows), a.shape[0], a.stride(0), b.data_ptr(), _dt(b),
+         _ptr(b_scale),
          N * K, N, K, seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, c.data_ptr(), _dt(c),
          tile, _stream(a))
     return c

@@ -90,11 +90,12 @@ int eimoe_gather(const void* x, int dtype, int H, const int32_t* rows, const int
 /* Grouped gate/up GEMM with SiLU*mul fused:  h[r,:] = silu(g) * u, [g|u] = a[row(r)] . W_gu[e]^T
  * for r in segment s (rows [seg_offsets[s], seg_offsets[s+1])), e = s % e_mod.
  * Replaces fused_moe.py:445-459 (first fused_moe_kernel launch + silu(g)*u).
- * a: bf16, row r reads a[(a_rows ? a_rows[r] : r) * lda + :H] (a_rows gathers tokens directly).
+ * a: bf16 [a_nrows, lda], row r reads a[(a_rows ? a_rows[r] : r) * lda + :H] (a_rows gathers tokens
+ * directly; every a_rows entry must be < a_nrows, reads beyond the buffer return 0).
  * w_gate_up: [E_w, 2I, H] bf16 or fp8 (rows [0,I) gate, [I,2I) up, fused_moe.py:91-101);
  * w_scale: fp8 only, [E_w, 2I] fp32 per-output-channel scales.  h: bf16 [max_rows, I].
  * H % 64 == 0, I % 32 == 0.  max_rows bounds seg_offsets[n_seg]. */
-int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int lda, const void* w_gate_up, int w_dtype,
+int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* w_gate_up, int w_dtype,
                             const float* w_scale, int H, int I, const int32_t* seg_offsets, int n_seg, int e_mod,
                             int max_rows, void* h, int tile, void* stream);
 
@@ -108,9 +109,10 @@ int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const
 
 /* Plain grouped GEMM, the X_grouped_gemm_single(A, B_list, block_sizes) contract
  * (single_group_gemm_moe.py:76-91): c[rows_s] = a[rows_s] . B[s % e_mod]^T with B packed as
- * [E_w, N, K] (b_expert_stride elements apart).  a bf16; b bf16/fp8 (+b_scale [E_w,N]);
+ * [E_w, N, K] (b_expert_stride elements apart).  a bf16 [a_nrows, lda] (rows gathered through a_rows
+ * when given); b bf16/fp8 (+b_scale [E_w,N]);
  * c f32 or bf16 [max_rows, N].  K % 64 == 0, N % 64 == 0. */
-int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int lda, const void* b, int b_dtype,
+int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* b, int b_dtype,
                        const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
                        int n_seg, int e_mod, int max_rows, void* c, int c_dtype, int tile, void* stream);
 

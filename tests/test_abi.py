@@ -1,0 +1,127 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+declared in include/eimoe.h, and rejects bad arguments on the host before any
+launch (error codes + messages), mirroring the reference's argument checks
+(e.g. blocks/moe/base.py:145-146, modules/moe/base.py:67-68)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from easyinfra_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "eimoe.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(eimoe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_abi_version():
+    lib = _lib.lib()
+    assert lib.eimoe_abi_version() == 1
+
+
+def test_every_header_function_is_exported_and_bound():
+    names = header_functions()
+    assert len(names) >= 12
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for n in names:
+        assert hasattr(raw, n), f"{n} declared in eimoe.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def _rc(name, *args):
+    return getattr(_lib.lib(), name)(*args)
+
+
+def test_router_validation():
+    assert _rc("eimoe_router_topk", None, 4, 8, 9, 1, None, None, None) == _lib.ERR_SHAPE
+    assert "k=9" in _lib.last_error()
+    assert _rc("eimoe_router_topk", None, 4, 600, 2, 1, None, None, None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_router_topk", None, 4, 8, 2, 1, None, None, None) == _lib.ERR_NULL
+    assert "logits" in _lib.last_error()
+    assert _rc("eimoe_router_topk", None, 0, 8, 2, 1, None, None, None) == _lib.EIMOE_OK  # empty batch
+    assert _rc("eimoe_router_topk", None, -1, 8, 2, 1, None, None, None) == _lib.ERR_SHAPE
+
+
+def test_align_validation():
+    assert _rc("eimoe_align", None, 4, 2, 0, 0, None, None, None, None, None, None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_align", None, 4, 2, -1, 8, None, None, None, None, None, None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_align", None, 4, 40, 0, 8, None, None, None, None, None, None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_align", None, 4, 2, 0, 8, None, None, None, None, None, None) == _lib.ERR_NULL
+
+
+def test_gemm_validation():
+    # H not a multiple of 64
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 100, 1, _lib.BF16, None, 100, 64, 1, 1, 1, 4, 1, 0,
+               None) == _lib.ERR_ALIGN
+    # I not a multiple of 32
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.BF16, None, 128, 40, 1, 1, 1, 4, 1, 0,
+               None) == _lib.ERR_ALIGN
+    # fp8 weights need scales
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.FP8, None, 128, 64, 1, 1, 1, 4, 1, 0,
+               None) == _lib.ERR_NULL
+    # bad dtype / segment count / tile
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, 7, None, 128, 64, 1, 1, 1, 4, 1, 0,
+               None) == _lib.ERR_DTYPE
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.BF16, None, 128, 64, 1, 2000, 1, 4, 1, 0,
+               None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.BF16, None, 128, 64, 1, 1, 1, 4, 1, 9,
+               None) == _lib.ERR_SHAPE
+    # tile whose output width does not divide I
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.BF16, None, 128, 96, 1, 1, 1, 4, 1,
+               _lib.TILE_256x256, None) == _lib.ERR_ALIGN
+    # down: I must be a multiple of 64*k_split
+    assert _rc("eimoe_gemm_down", 1, 192, 1, _lib.BF16, None, 128, 1, 1, 1, 4, 1, _lib.F32, 2, 0,
+               None) == _lib.ERR_ALIGN
+    assert _rc("eimoe_gemm_down", 1, 192, 1, _lib.BF16, None, 128, 1, 1, 1, 4, 1, 5, 1, 0, None) == _lib.ERR_DTYPE
+    # zero rows is a no-op
+    assert _rc("eimoe_gemm_down", None, 192, None, _lib.BF16, None, 128, None, 1, 1, 0, None, _lib.F32, 1, 0,
+               None) == _lib.EIMOE_OK
+
+
+def test_combine_and_quant_validation():
+    assert _rc("eimoe_combine", 1, _lib.F32, 1, 0, 1, 1, 4, 2, 100, None, 0, 1, _lib.F32, None) == _lib.ERR_ALIGN
+    assert _rc("eimoe_combine", 1, 3, 1, 0, 1, 1, 4, 2, 128, None, 0, 1, _lib.F32, None) == _lib.ERR_DTYPE
+    assert _rc("eimoe_combine", None, _lib.F32, 1, 0, 1, 1, 4, 2, 128, None, 0, 1, _lib.F32, None) == _lib.ERR_NULL
+    assert _rc("eimoe_quantize_rows_fp8", None, _lib.FP8, 4, 4, None, None, None) == _lib.ERR_DTYPE
+    assert _rc("eimoe_quantize_rows_fp8", None, _lib.F32, 0, 4, None, None, None) == _lib.EIMOE_OK
+
+
+def test_fused_validation_and_workspace():
+    f = "eimoe_fused_moe"
+    base = dict(x=1, logits=1, T=16, H=256, I=128, E=8, k=2, wgu=1, wd=1, wdt=_lib.BF16, sgu=None, sd=None, e_lo=0,
+                n_local=8, shgu=None, shd=None, Is=0, flags=1, out=1, odt=_lib.BF16, ws=1, wsb=1 << 30, ids=None,
+                w=None, stream=None)
+
+    def call(**kw):
+        a = dict(base, **kw)
+        return _rc(f, *a.values())
+
+    assert call(k=9) == _lib.ERR_SHAPE
+    assert call(e_lo=4, n_local=8) == _lib.ERR_SHAPE            # window outside [0,E)
+    assert call(H=100) == _lib.ERR_ALIGN
+    assert call(I=96) == _lib.ERR_ALIGN
+    assert call(wdt=_lib.FP8) == _lib.ERR_NULL                   # fp8 without scales
+    assert call(Is=256) == _lib.ERR_NULL                         # shared size without weights
+    assert call(wsb=16) == _lib.ERR_WORKSPACE
+    assert "workspace" in _lib.last_error()
+    assert call(T=0) == _lib.EIMOE_OK
+    ws = _lib.lib().eimoe_fused_moe_workspace_bytes(16, 256, 128, 8, 2, 8, 0, _lib.BF16, 1)
+    ws_sh = _lib.lib().eimoe_fused_moe_workspace_bytes(16, 256, 128, 8, 2, 8, 256, _lib.BF16, 1)
+    ws_f32 = _lib.lib().eimoe_fused_moe_workspace_bytes(16, 256, 128, 8, 2, 8, 0, _lib.F32, 1)
+    assert 0 < ws < ws_sh and ws < ws_f32
+    # h (A*I bf16) and y (A*H) dominate: at least that much
+    assert ws >= 32 * 128 * 2 + 32 * 256 * 2
+
+
+def test_ops_refuse_cpu_tensors():
+    torch = pytest.importorskip("torch")
+    from easyinfra_amd import ops
+    with pytest.raises(ValueError):
+        ops.router_topk(torch.zeros(4, 8), 2)
