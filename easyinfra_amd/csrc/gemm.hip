@@ -191,12 +191,13 @@ struct Geo {
   }
 };
 
-// 16-byte chunk swizzle inside a 128-byte LDS row.  Fragment reads touch 16
-// consecutive rows at one logical chunk; with this XOR every aligned group of 8 rows,
-// and the even and odd rows of every aligned group of 16, land on distinct chunks, so
-// ds_read_b128 is conflict-free whether the LDS serves 8 lanes over 32 banks or 16
-// lanes over 64 banks per cycle.
-__device__ __forceinline__ int swz(int R) { return (R ^ (R >> 3)) & 7; }
+// 16-byte chunk swizzle inside a 128-byte LDS row.  A fragment read (ds_read_b128)
+// touches 16 consecutive rows at chunk q (lanes 0-15), q+1 (16-31), ...; XOR with row&7
+// makes it conflict-free on gfx950 (measured with SQ_LDS_BANK_CONFLICT: 4 cycles per
+// instruction, the 1 KiB/4-cycle floor; swizzles mixing in higher row bits measured
+// 2-way conflicts).  It depends on R mod 8 only, so all fragments of a wave share one
+// address pattern and differ by immediate offsets.
+__device__ __forceinline__ int swz(int R) { return R & 7; }
 
 template <class G>
 __device__ __forceinline__ void read_frags(const uint16_t* sA, const uint16_t* sB, int kk, int wm, int wn, int lane,
@@ -223,6 +224,18 @@ __device__ __forceinline__ void mma(f32x4_t (&acc)[G::MB][G::NB], const bf16x8_t
 #pragma unroll
     for (int j = 0; j < G::NB; ++j)
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+}
+
+// One 64-wide K slab: two 32-wide MFMA steps, each reading its fragments first.
+template <class G>
+__device__ __forceinline__ void slab_mma(f32x4_t (&acc)[G::MB][G::NB], const uint16_t* sA, const uint16_t* sB, int wm,
+                                         int wn, int lane) {
+#pragma unroll
+  for (int kk = 0; kk < G::BK / 32; ++kk) {
+    bf16x8_t af[G::MB], bfr[G::NB];
+    read_frags<G>(sA, sB, kk, wm, wn, lane, af, bfr);
+    mma<G>(acc, af, bfr);
+  }
 }
 
 // Epilogue: lane owns rows 4*(lane/16)+r of each 16-row fragment and NI adjacent columns.
@@ -337,8 +350,14 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
   constexpr int B_PW = BN / 8 / G::NW;
   static_assert(A_PW * 8 * G::NW == BM && B_PW * 8 * G::NW == BN, "slab split over waves");
 
-  __shared__ __attribute__((aligned(1024))) uint16_t sA[2][BM * BK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sB[2][BN * BK];
+  // The two LDS stages are distinct objects, and the loop below is unrolled by two so
+  // the stage being read is known statically: alias analysis can then prove the DMA
+  // into one stage does not touch the other, and the compiler does not wait for the
+  // in-flight DMA before reading the current stage.
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[BN * BK];
   __shared__ int s_pref[kMaxSeg + 1];
 
   TileCoord tc;
@@ -379,18 +398,18 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
     for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int KT = p.K / BK;
-  issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA[0], sB[0], wave, 0);
+  issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, 0);
   __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA[cur ^ 1], sB[cur ^ 1], wave, (kt + 1) * BK * 2);
-    bf16x8_t a0[G::MB], b0[G::NB], a1[G::MB], b1[G::NB];
-    read_frags<G>(sA[cur], sB[cur], 0, wm, wn, lane, a0, b0);
-    read_frags<G>(sA[cur], sB[cur], 1, wm, wn, lane, a1, b1);
-    mma<G>(acc, a0, b0);
-    mma<G>(acc, a1, b1);
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {   // stage kt is in buffer 0 here
+    issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA1, sB1, wave, (kt + 1) * BK * 2);
+    slab_mma<G>(acc, sA0, sB0, wm, wn, lane);
+    __syncthreads();
+    if (kt + 2 < KT) issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, (kt + 2) * BK * 2);
+    slab_mma<G>(acc, sA1, sB1, wm, wn, lane);
     __syncthreads();
   }
+  if (kt < KT) slab_mma<G>(acc, sA0, sB0, wm, wn, lane);   // odd slab count: last slab in buffer 0
   epilogue<G, EPI>(p, tc, acc, wm, wn, lane, nullptr);
 }
 
