@@ -1,0 +1,262 @@
+"""Pins the CPU oracle (CPU-only tests).
+
+The reference ships no tests, golden vectors or fixtures for this path, so each
+oracle function is checked against an independent statement of the same math:
+brute-force loops in float64, the reference's literal torch ops where they are
+deterministic, closed forms, and invariants (EP decomposition, linearity,
+permutation identities) chosen so that a dropped term, a wrong index or a
+swapped operand fails at least one check.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from easyinfra_amd.workloads import SHAPES, make_inputs
+
+
+# --------------------------------------------------------------------------- router
+def _brute_route(logits, k, renorm):
+    T, E = logits.shape
+    ids = np.zeros((T, k), dtype=np.int64)
+    w = np.zeros((T, k), dtype=np.float64)
+    for t in range(T):
+        row = [float(v) for v in logits[t]]
+        order = sorted(range(E), key=lambda e: (-row[e], e))[:k]
+        m = max(row)
+        ex = [math.exp(v - m) for v in row]
+        tot = sum(ex)
+        sel = [ex[e] for e in order]
+        den = sum(sel) if renorm else tot
+        ids[t] = order
+        w[t] = [v / den for v in sel]
+    return ids, w
+
+
+@pytest.mark.parametrize("T,E,k,renorm", [(7, 8, 2, True), (9, 64, 6, False), (5, 128, 8, True), (4, 3, 3, False)])
+def test_route_topk_brute_force(T, E, k, renorm):
+    g = torch.Generator().manual_seed(T * E)
+    logits = torch.randn(T, E, generator=g) * 3
+    ids, w = oracle.route_topk(logits, k, renorm)
+    bi, bw = _brute_route(logits.double().numpy(), k, renorm)
+    assert np.array_equal(ids.numpy(), bi)
+    np.testing.assert_allclose(w.numpy(), bw, rtol=2e-6, atol=1e-8)
+
+
+def test_route_topk_matches_reference_ops_on_tie_free_inputs():
+    """modeling_qwen3_moe.py:260-263 literally: softmax(fp32) -> topk -> /sum."""
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn(300, 64, generator=g)
+    p = torch.softmax(logits, dim=-1, dtype=torch.float32)
+    rw, ri = torch.topk(p, 6, dim=-1)
+    rw = rw / rw.sum(-1, keepdim=True)
+    ids, w = oracle.route_topk(logits, 6, True)
+    assert torch.equal(ids.long(), ri)
+    torch.testing.assert_close(w, rw, rtol=1e-6, atol=1e-8)
+
+
+def test_route_topk_ties_and_closed_forms():
+    logits = torch.tensor([[2.0, 2.0, 1.0, 2.0], [0.0, 0.0, 0.0, 0.0]])
+    ids, w = oracle.route_topk(logits, 2, True)
+    assert ids.tolist() == [[0, 1], [0, 1]]
+    torch.testing.assert_close(w, torch.full((2, 2), 0.5))
+    # two experts, top-1 without renorm: weight = sigmoid(l0 - l1)
+    l = torch.tensor([[1.3, -0.4]])
+    _, w = oracle.route_topk(l, 1, False)
+    assert abs(float(w[0, 0]) - 1 / (1 + math.exp(-1.7))) < 1e-6
+
+
+def test_route_topk_invariants():
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(200, 32, generator=g)
+    ids, w = oracle.route_topk(logits, 5, True)
+    assert torch.all(w[:, :-1] >= w[:, 1:])
+    torch.testing.assert_close(w.sum(-1), torch.ones(200))
+    assert all(len(set(r)) == 5 for r in ids.tolist())
+
+
+# --------------------------------------------------------------------------- align
+def _brute_align(ids, n_loc, e_lo):
+    T, k = ids.shape
+    flat = ids.reshape(-1)
+    order = []
+    counts = []
+    for e in range(n_loc):
+        hit = [i for i in range(T * k) if flat[i] == e + e_lo]
+        counts.append(len(hit))
+        order += hit
+    pos = [-1] * (T * k)
+    for r, i in enumerate(order):
+        pos[i] = r
+    return counts, order, pos
+
+
+@pytest.mark.parametrize("T,k,E,e_lo,n_loc", [(13, 2, 8, 0, 8), (20, 6, 64, 0, 64), (17, 8, 128, 32, 32), (5, 3, 4, 1, 2)])
+def test_align_brute_force(T, k, E, e_lo, n_loc):
+    g = torch.Generator().manual_seed(T + E)
+    ids = torch.rand(T, E, generator=g).argsort(1)[:, :k].numpy()
+    al = oracle.align(ids, n_loc, e_lo)
+    counts, order, pos = _brute_align(ids, n_loc, e_lo)
+    assert al["counts"].tolist() == counts
+    assert al["offsets"].tolist() == list(np.concatenate([[0], np.cumsum(counts)]))
+    assert al["sorted_flat"].tolist() == order
+    assert al["pos"].tolist() == pos
+    assert al["sorted_tok"].tolist() == [i // k for i in order]
+    assert al["sorted_slot"].tolist() == [i % k for i in order]
+
+
+def test_align_matches_stable_sort_and_scatter_add():
+    """moe_all2all.py:346 (with stable=True) and blocks/moe/base.py:357-359."""
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, 16, (500, 4), generator=g)
+    al = oracle.align(ids.numpy(), 16, 0)
+    idx = ids.view(-1).sort(stable=True).indices
+    assert al["sorted_flat"].tolist() == idx.tolist()
+    counts = torch.zeros(16, dtype=torch.int64).scatter_add_(0, ids.view(-1), torch.ones(2000, dtype=torch.int64))
+    assert al["counts"].tolist() == counts.tolist()
+
+
+def test_align_permutation_identities():
+    g = torch.Generator().manual_seed(11)
+    ids = torch.randint(0, 40, (333, 3), generator=g).numpy()
+    al = oracle.align(ids, 32, 4)
+    sf, pos = al["sorted_flat"], al["pos"]
+    assert np.array_equal(pos[sf], np.arange(sf.size))
+    local = (ids.reshape(-1) >= 4) & (ids.reshape(-1) < 36)
+    assert np.array_equal(np.sort(sf), np.nonzero(local)[0])
+    assert np.all(pos[~local] == -1)
+    seg = np.repeat(np.arange(32), al["counts"])
+    assert np.array_equal(ids.reshape(-1)[sf] - 4, seg)
+
+
+# --------------------------------------------------------------------------- experts
+def test_silu_closed_forms():
+    x = torch.tensor([0.0, 1.0, -1.0, 30.0, -30.0])
+    s = oracle.silu(x)
+    ref = torch.tensor([0.0, 1 / (1 + math.exp(-1)), -1 / (1 + math.exp(1)), 30.0, 0.0])
+    torch.testing.assert_close(s, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_expert_mlp_float64_loops():
+    g = torch.Generator().manual_seed(5)
+    M, H, I = 3, 6, 4
+    x = torch.randn(M, H, generator=g)
+    wgu = torch.randn(2 * I, H, generator=g)
+    wd = torch.randn(H, I, generator=g)
+    y = oracle.expert_mlp(x, wgu, wd)
+    X, Wg, Wd = x.double().numpy(), wgu.double().numpy(), wd.double().numpy()
+    ref = np.zeros((M, H))
+    for m in range(M):
+        h = []
+        for i in range(I):
+            gv = sum(X[m, j] * Wg[i, j] for j in range(H))
+            uv = sum(X[m, j] * Wg[I + i, j] for j in range(H))
+            h.append(gv / (1 + math.exp(-gv)) * uv)
+        for o in range(H):
+            ref[m, o] = sum(h[i] * Wd[o, i] for i in range(I))
+    np.testing.assert_allclose(y.numpy(), ref, rtol=1e-4, atol=1e-5)
+
+
+def test_expert_mlp_gate_up_halves_are_not_interchangeable():
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(4, 8, generator=g)
+    wgu = torch.randn(10, 8, generator=g)
+    wd = torch.randn(8, 5, generator=g)
+    swapped = torch.cat([wgu[5:], wgu[:5]])
+    assert not torch.allclose(oracle.expert_mlp(x, wgu, wd), oracle.expert_mlp(x, swapped, wd))
+
+
+# --------------------------------------------------------------------------- layer
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_moe_forward_vs_dense_float64(name):
+    inp = make_inputs(SHAPES[name], 11, device="cpu", hidden=64, inter=32)
+    s = inp.shape
+    a = oracle.moe_forward(inp.x, inp.logits, s.top_k, inp.w_gate_up, inp.w_down, s.renormalize,
+                           inp.shared_gate_up, inp.shared_down, inp.expert_range)
+    b = oracle.moe_forward_dense(inp.x, inp.logits, s.top_k, inp.w_gate_up, inp.w_down, s.renormalize,
+                                 inp.shared_gate_up, inp.shared_down, inp.expert_range)
+    np.testing.assert_allclose(a.double().numpy(), b.numpy(), rtol=1e-4, atol=1e-6)
+
+
+def test_moe_forward_expert_parallel_decomposition():
+    """Summing the EP shares of disjoint expert windows gives the whole layer."""
+    inp = make_inputs(SHAPES["mixtral-8x7b"], 17, device="cpu", hidden=64, inter=32)
+    s = inp.shape
+    full = oracle.moe_forward(inp.x, inp.logits, 2, inp.w_gate_up, inp.w_down, True)
+    parts = sum(oracle.moe_forward(inp.x, inp.logits, 2, inp.w_gate_up[lo:lo + 4], inp.w_down[lo:lo + 4], True,
+                                   expert_range=(lo, lo + 4)) for lo in (0, 4))
+    torch.testing.assert_close(parts, full, rtol=1e-5, atol=1e-6)
+
+
+def test_moe_forward_subset_shared_and_linearity():
+    inp = make_inputs(SHAPES["deepseek-v2-lite"], 9, device="cpu", hidden=64, inter=32)
+    s = inp.shape
+    args = (inp.x, inp.logits, s.top_k, inp.w_gate_up, inp.w_down, s.renormalize)
+    full = oracle.moe_forward(*args, inp.shared_gate_up, inp.shared_down)
+    sub = torch.tensor([7, 2, 5])
+    part = oracle.moe_forward(*args, inp.shared_gate_up, inp.shared_down, token_subset=sub)
+    torch.testing.assert_close(part, full[sub])
+    no_sh = oracle.moe_forward(*args)
+    torch.testing.assert_close(full, no_sh + oracle.shared_mlp(inp.x.float(), inp.shared_gate_up, inp.shared_down),
+                               rtol=1e-5, atol=1e-6)
+    twice = oracle.moe_forward(inp.x, inp.logits, s.top_k, inp.w_gate_up, 2 * inp.w_down, s.renormalize)
+    torch.testing.assert_close(twice, 2 * no_sh, rtol=1e-5, atol=1e-6)
+
+
+def test_moe_forward_no_local_expert_gives_zero_rows():
+    inp = make_inputs(SHAPES["qwen3-30b-a3b-local32"], 200, device="cpu", hidden=64, inter=32)
+    out, parts = oracle.moe_forward(inp.x, inp.logits, 8, inp.w_gate_up, inp.w_down, True,
+                                    expert_range=(0, 32), return_parts=True)
+    none_local = ~(parts["ids"] < 32).any(1)
+    assert none_local.any()
+    assert torch.count_nonzero(out[none_local]) == 0
+
+
+# --------------------------------------------------------------------------- fp8
+def test_quantize_rows_fp8_exact_values_and_rne_ties():
+    # absmax 448 -> scale 1: values are quantised as themselves
+    x = torch.tensor([[448.0, 1.0625, 1.1875, -2.5, 0.0, 0.013671875]])
+    q, s = oracle.quantize_rows_fp8(x)
+    assert float(s[0]) == 1.0
+    # 1.0625 is halfway between 1.0 and 1.125 -> even mantissa (1.0);
+    # 1.1875 halfway between 1.125 and 1.25 -> even (1.25); 0.013671875 = 7*2^-9 is an e4m3 subnormal
+    assert q.float().tolist() == [[448.0, 1.0, 1.25, -2.5, 0.0, 0.013671875]]
+
+
+def test_quantize_rows_fp8_scale_and_error_bound():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(50, 300, generator=g) * 0.02
+    x[3] = 0
+    q, s = oracle.quantize_rows_fp8(x)
+    amax = x.abs().amax(1)
+    torch.testing.assert_close(s[amax > 0], (amax / 448.0)[amax > 0])
+    assert float(s[3]) == 1.0 and torch.count_nonzero(q[3].float()) == 0
+    deq = q.float() * s[:, None]
+    # e4m3: 3 mantissa bits -> relative error <= 2^-4 for normal values, absolute 2^-10*s below
+    err = (deq - x).abs()
+    bound = torch.maximum(x.abs() * 2 ** -4, (2 ** -10) * s[:, None])
+    assert torch.all(err <= bound * 1.0001)
+    assert torch.all(q.float().abs() <= 448)
+
+
+def test_fp8_forward_with_exactly_representable_weights_matches_bf16():
+    """W8A16 on weights that are already e4m3 values times their scale equals the bf16 layer."""
+    inp = make_inputs(SHAPES["mixtral-8x7b"], 8, device="cpu", hidden=64, inter=32)
+    qgu, sgu = oracle.quantize_weights_fp8(inp.w_gate_up.float())
+    qd, sd = oracle.quantize_weights_fp8(inp.w_down.float())
+    wgu = qgu.float() * sgu[..., None]
+    wd = qd.float() * sd[..., None]
+    a = oracle.moe_forward_fp8(inp.x, inp.logits, 2, qgu, sgu, qd, sd, True, mode="w8a16")
+    b = oracle.moe_forward(inp.x, inp.logits, 2, wgu, wd, True, round_h_bf16=True)
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+
+
+def test_grouped_gemm_single_contract():
+    g = torch.Generator().manual_seed(4)
+    a = torch.randn(9, 5, generator=g)
+    bs = [torch.randn(3, 5, generator=g) for _ in range(3)]
+    out = oracle.grouped_gemm(a, bs, [4, 0, 5])
+    torch.testing.assert_close(out[:4], a[:4] @ bs[0].T)
+    torch.testing.assert_close(out[4:], a[4:] @ bs[2].T)
