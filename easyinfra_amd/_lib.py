@@ -14,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libeimoe.so")
 EIMOE_OK = 0
 ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_WORKSPACE, ERR_HIP = -1, -2, -3, -4, -5, -6
 F32, BF16, FP8 = 0, 1, 2
-RENORMALIZE, Y_F32 = 1, 2
+RENORMALIZE, Y_F32, W8A8 = 1, 2, 4
 TILE_AUTO, TILE_256x256, TILE_128x128, TILE_32x128, TILE_16x64 = 0, 1, 2, 3, 4
 MAX_TOPK, MAX_EXPERTS, MAX_SEGMENTS = 32, 512, 1024
 
@@ -34,6 +34,10 @@ SIGNATURES = {
                                         c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p]),
     "eimoe_gemm_down": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_int, c_int,
                                 c_void_p, c_int, c_int, c_int, c_void_p]),
+    "eimoe_gemm_gate_up_silu_w8a8": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int,
+                                             c_int, c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p]),
+    "eimoe_gemm_down_w8a8": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int,
+                                     c_int, c_void_p, c_int, c_int, c_int, c_void_p]),
     "eimoe_grouped_gemm": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_longlong, c_int,
                                    c_int,
                                    c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_int, c_void_p]),

@@ -70,7 +70,7 @@ int pick_down_split(int max_rows, int n_local, int H, int I) {
 }
 
 struct FusedLayout {
-  size_t ids, w, counts, offsets, sorted_flat, sorted_tok, pos, h, y, sh_off, sh_h, sh_y, total;
+  size_t ids, w, counts, offsets, sorted_flat, sorted_tok, pos, h, y, sh_off, sh_h, sh_y, xq, sx, hq, sh, total;
   int k_split;
   int y_dtype;
 };
@@ -79,7 +79,7 @@ FusedLayout fused_layout(int T, int H, int I, int k, int n_local, int Is, int ou
   FusedLayout L{};
   const size_t A = static_cast<size_t>(T) * k;
   L.y_dtype = ((flags & EIMOE_Y_F32) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
-  L.k_split = pick_down_split(static_cast<int>(A), n_local, H, I);
+  L.k_split = pick_down_split(static_cast<int>(A), n_local, H, (flags & EIMOE_W8A8) ? I / 2 : I);
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -95,6 +95,12 @@ FusedLayout fused_layout(int T, int H, int I, int k, int n_local, int Is, int ou
   L.pos = take(A * 4);
   L.h = take(A * I * 2);
   L.y = take(static_cast<size_t>(L.k_split) * A * H * elem_size(L.y_dtype));
+  if (flags & EIMOE_W8A8) {
+    L.xq = take(static_cast<size_t>(T) * H);
+    L.sx = take(static_cast<size_t>(T) * 4);
+    L.hq = take(A * I);
+    L.sh = take(A * 4);
+  }
   if (Is > 0) {
     L.sh_off = take(2 * 4);
     L.sh_h = take(static_cast<size_t>(T) * Is * 2);
@@ -113,7 +119,7 @@ __global__ void dense_segment_kernel(int32_t* off, int T) {
 
 int run_gate_up(const void* a, const int32_t* a_rows, long long a_nrows, int lda, const void* w, int w_dtype,
                 const float* w_scale, int H, int I, const int32_t* seg, int n_seg, int e_mod, int max_rows, void* h,
-                int tile, hipStream_t s) {
+                int tile, hipStream_t s, const float* a_scale = nullptr) {
   GemmArgs p{};
   p.a = a;
   p.a_rows = a_rows;
@@ -135,11 +141,14 @@ int run_gate_up(const void* a, const int32_t* a_rows, long long a_nrows, int lda
   p.k_split = 1;
   p.max_rows = max_rows;
   p.a_rows_cap = a_rows ? a_nrows : max_rows;
-  return hip_check(launch_grouped_gemm(p, kEpiSiluBF16, w_dtype == EIMOE_FP8, max_rows, tile, s), "gate_up gemm");
+  p.a_scale = a_scale;
+  return hip_check(launch_grouped_gemm(p, kEpiSiluBF16, w_dtype == EIMOE_FP8, a_scale != nullptr, max_rows, tile, s),
+                   "gate_up gemm");
 }
 
 int run_down(const void* h, int I, const void* w, int w_dtype, const float* w_scale, int H, const int32_t* seg,
-             int n_seg, int e_mod, int max_rows, void* y, int y_dtype, int k_split, int tile, hipStream_t s) {
+             int n_seg, int e_mod, int max_rows, void* y, int y_dtype, int k_split, int tile, hipStream_t s,
+             const float* h_scale = nullptr) {
   GemmArgs p{};
   p.a = h;
   p.a_rows = nullptr;
@@ -161,8 +170,10 @@ int run_down(const void* h, int I, const void* w, int w_dtype, const float* w_sc
   p.k_split = k_split;
   p.max_rows = max_rows;
   p.a_rows_cap = max_rows;
+  p.a_scale = h_scale;
   const int epi = y_dtype == EIMOE_F32 ? kEpiStoreF32 : kEpiStoreBF16;
-  return hip_check(launch_grouped_gemm(p, epi, w_dtype == EIMOE_FP8, max_rows, tile, s), "down gemm");
+  return hip_check(launch_grouped_gemm(p, epi, w_dtype == EIMOE_FP8, h_scale != nullptr, max_rows, tile, s),
+                   "down gemm");
 }
 
 }  // namespace
@@ -286,6 +297,54 @@ int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const
                   S(stream));
 }
 
+int eimoe_gemm_gate_up_silu_w8a8(const void* a, const float* a_scale, const int32_t* a_rows, int a_nrows, int lda,
+                                 const void* w_gate_up, const float* w_scale, int H, int I,
+                                 const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows, void* h, int tile,
+                                 void* stream) {
+  int rc = check_gemm_common(max_rows, n_seg, e_mod);
+  if (rc) return rc;
+  if (H < 128 || H % 128) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 128", H);
+  if (I < 32 || I % 32) return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 32", I);
+  if (lda < H || lda % 16) return fail(EIMOE_ERR_SHAPE, "lda=%d must be >= H=%d and a multiple of 16", lda, H);
+  if (a_rows && a_nrows < 1) return fail(EIMOE_ERR_SHAPE, "a_nrows=%d < 1 with a row map", a_nrows);
+  if (!a_rows) a_nrows = max_rows;
+  if (static_cast<long long>(a_nrows) * lda > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "A buffer exceeds 2 GiB");
+  if (2ll * I * H > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "one expert's gate/up weights exceed 2 GiB");
+  if ((rc = check_tile(tile, kEpiSiluBF16, I))) return rc;
+  if (max_rows == 0) return EIMOE_OK;
+  REQUIRE_PTR(a);
+  REQUIRE_PTR(a_scale);
+  REQUIRE_PTR(w_gate_up);
+  REQUIRE_PTR(w_scale);
+  REQUIRE_PTR(seg_offsets);
+  REQUIRE_PTR(h);
+  return run_gate_up(a, a_rows, a_nrows, lda, w_gate_up, EIMOE_FP8, w_scale, H, I, seg_offsets, n_seg, e_mod,
+                     max_rows, h, tile, S(stream), a_scale);
+}
+
+int eimoe_gemm_down_w8a8(const void* hq, const float* h_scale, int I, const void* w_down, const float* w_scale, int H,
+                         const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows, void* y, int y_dtype,
+                         int k_split, int tile, void* stream) {
+  int rc = check_gemm_common(max_rows, n_seg, e_mod);
+  if (rc) return rc;
+  if (y_dtype != EIMOE_BF16 && y_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "y_dtype=%d", y_dtype);
+  if (H < 64 || H % 64) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 64", H);
+  if (k_split < 1 || k_split > 64) return fail(EIMOE_ERR_SHAPE, "k_split=%d outside [1,64]", k_split);
+  if (I < 128 || I % (128 * k_split))
+    return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 128*k_split=%d", I, 128 * k_split);
+  if ((rc = check_tile(tile, kEpiStoreF32, H))) return rc;
+  if (static_cast<long long>(max_rows) * I > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "hq exceeds 2 GiB");
+  if (max_rows == 0) return EIMOE_OK;
+  REQUIRE_PTR(hq);
+  REQUIRE_PTR(h_scale);
+  REQUIRE_PTR(w_down);
+  REQUIRE_PTR(w_scale);
+  REQUIRE_PTR(seg_offsets);
+  REQUIRE_PTR(y);
+  return run_down(hq, I, w_down, EIMOE_FP8, w_scale, H, seg_offsets, n_seg, e_mod, max_rows, y, y_dtype, k_split,
+                  tile, S(stream), h_scale);
+}
+
 int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* b, int b_dtype,
                        const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
                        int n_seg, int e_mod, int max_rows, void* c, int c_dtype, int tile, void* stream) {
@@ -331,7 +390,8 @@ int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int ld
   p.max_rows = max_rows;
   p.a_rows_cap = a_nrows;
   const int epi = c_dtype == EIMOE_F32 ? kEpiStoreF32 : kEpiStoreBF16;
-  return hip_check(launch_grouped_gemm(p, epi, b_dtype == EIMOE_FP8, max_rows, tile, S(stream)), "grouped_gemm");
+  return hip_check(launch_grouped_gemm(p, epi, b_dtype == EIMOE_FP8, false, max_rows, tile, S(stream)),
+                   "grouped_gemm");
 }
 
 int eimoe_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
@@ -391,6 +451,9 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
   if (out_dtype != EIMOE_BF16 && out_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "out_dtype=%d", out_dtype);
   if (static_cast<long long>(T) * k > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "T*k overflows int32");
+  if ((flags & EIMOE_W8A8) && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "EIMOE_W8A8 needs fp8 weights");
+  if ((flags & EIMOE_W8A8) && (H % 128 || I % 128))
+    return fail(EIMOE_ERR_ALIGN, "W8A8 needs H=%d and I=%d multiples of 128", H, I);
   if (T == 0) return EIMOE_OK;
   REQUIRE_PTR(x);
   REQUIRE_PTR(logits);
@@ -427,12 +490,28 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos, s),
                       "align")))
     return rc;
-  if ((rc = run_gate_up(x, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local, A,
-                        at(L.h), EIMOE_TILE_AUTO, s)))
-    return rc;
-  if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y), L.y_dtype,
-                     L.k_split, EIMOE_TILE_AUTO, s)))
-    return rc;
+  if (flags & EIMOE_W8A8) {
+    // activations quantised per token (x) and per row (h); both GEMMs on the fp8 MFMA
+    uint8_t* xq = static_cast<uint8_t*>(at(L.xq));
+    float* sx = static_cast<float*>(at(L.sx));
+    uint8_t* hq = static_cast<uint8_t*>(at(L.hq));
+    float* sh = static_cast<float*>(at(L.sh));
+    if ((rc = hip_check(launch_quantize_rows_fp8(x, kBF16, T, H, xq, sx, s), "quantize x"))) return rc;
+    if ((rc = run_gate_up(xq, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
+                          A, at(L.h), EIMOE_TILE_AUTO, s, sx)))
+      return rc;
+    if ((rc = hip_check(launch_quantize_rows_fp8(at(L.h), kBF16, A, I, hq, sh, s), "quantize h"))) return rc;
+    if ((rc = run_down(hq, I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y), L.y_dtype,
+                       L.k_split, EIMOE_TILE_AUTO, s, sh)))
+      return rc;
+  } else {
+    if ((rc = run_gate_up(x, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
+                          A, at(L.h), EIMOE_TILE_AUTO, s)))
+      return rc;
+    if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y),
+                       L.y_dtype, L.k_split, EIMOE_TILE_AUTO, s)))
+      return rc;
+  }
   const void* sh_y = nullptr;
   if (shared_inter > 0) {
     int32_t* sh_off = static_cast<int32_t*>(at(L.sh_off));

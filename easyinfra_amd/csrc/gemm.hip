@@ -250,13 +250,15 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
     for (int r = 0; r < 4; ++r) {
       const int row = tc.row0 + wm * G::WM + i * 16 + lq * 4 + r;
       if (row >= tc.row_end) continue;
+      // fp8 activations: per-row scale of the A row this output row came from
+      const float rs = p.a_scale ? p.a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
       if constexpr (G::SILU) {
         const int col0 = tc.n_tile * G::OUT_BN + wn * (G::WN / 2) + lr * G::NI;
         float h[G::NI];
 #pragma unroll
         for (int j = 0; j < G::NI; ++j) {
-          float g = acc[i][j][r];
-          float u = acc[i][j + G::NI][r];
+          float g = acc[i][j][r] * rs;
+          float u = acc[i][j + G::NI][r] * rs;
           if (scale) {
             g *= scale[col0 + j];
             u *= scale[p.up_off + col0 + j];
@@ -268,7 +270,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
         const int col0 = tc.n_tile * G::OUT_BN + wn * G::WN + lr * G::NI;
         float v[G::NI];
 #pragma unroll
-        for (int j = 0; j < G::NI; ++j) v[j] = acc[i][j][r] * (scale ? scale[col0 + j] : 1.f);
+        for (int j = 0; j < G::NI; ++j) v[j] = acc[i][j][r] * rs * (scale ? scale[col0 + j] : 1.f);
         const long long off =
             static_cast<long long>(tc.split) * p.c_split_stride + static_cast<long long>(row) * p.ldc + col0;
         if constexpr (EPI == kEpiStoreF32) store_f32<G::NI>(static_cast<float*>(p.c) + off, v);
@@ -413,6 +415,117 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
   epilogue<G, EPI>(p, tc, acc, wm, wn, lane, nullptr);
 }
 
+// ---------------------------------------------------------------------------- fp8 x fp8 (W8A8)
+// Both operands OCP e4m3fn on v_mfma_scale_f32_16x16x128_f8f6f4 (block scales fixed at
+// 1.0; the per-row activation scale and per-output-channel weight scale are applied in
+// the epilogue).  A 128-wide fp8 K slab is one 128-byte LDS row, so slab loading,
+// swizzle and double buffering are those of the bf16 kernel.  Each lane feeds 32 bytes
+// per operand: 16-byte chunks q and q+4 of its row (lane group q = lane/16); A and B
+// use the same K assignment, so the K sum is exact whatever order the instruction adds.
+template <class G>
+__device__ __forceinline__ void read_frags_fp8(const uint8_t* sA, const uint8_t* sB, int wm, int wn, int lane,
+                                               i32x8_t (&af)[G::MB], i32x8_t (&bfr)[G::NB]) {
+  const int lr = lane & 15;
+  const int q = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < G::MB; ++i) {
+    const int R = wm * G::WM + i * 16 + lr;
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(&sA[R * 128 + ((q ^ swz(R)) << 4)]);
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(&sA[R * 128 + (((q + 4) ^ swz(R)) << 4)]);
+    af[i] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  }
+#pragma unroll
+  for (int j = 0; j < G::NB; ++j) {
+    const int R = wn * G::WN + j * 16 + lr;
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(&sB[R * 128 + ((q ^ swz(R)) << 4)]);
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(&sB[R * 128 + (((q + 4) ^ swz(R)) << 4)]);
+    bfr[j] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  }
+}
+
+template <class G>
+__device__ __forceinline__ void slab_mma_fp8(f32x4_t (&acc)[G::MB][G::NB], const uint8_t* sA, const uint8_t* sB,
+                                             int wm, int wn, int lane) {
+  i32x8_t af[G::MB], bfr[G::NB];
+  read_frags_fp8<G>(sA, sB, wm, wn, lane, af, bfr);
+#pragma unroll
+  for (int i = 0; i < G::MB; ++i)
+#pragma unroll
+    for (int j = 0; j < G::NB; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bfr[j], acc[i][j], 0, 0, 0, 127, 0, 127);
+}
+
+template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
+__global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8_kernel(GemmArgs p) {
+  using G = Geo<BM, BN, WGM, WGN, EPI>;
+  constexpr int BKB = 128;                    // K per slab = bytes per LDS row
+  constexpr int A_PW = BM / 8 / G::NW;
+  constexpr int B_PW = BN / 8 / G::NW;
+  static_assert(A_PW * 8 * G::NW == BM && B_PW * 8 * G::NW == BN, "slab split over waves");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t sA0[BM * BKB];
+  __shared__ __attribute__((aligned(1024))) uint8_t sA1[BM * BKB];
+  __shared__ __attribute__((aligned(1024))) uint8_t sB0[BN * BKB];
+  __shared__ __attribute__((aligned(1024))) uint8_t sB1[BN * BKB];
+  __shared__ int s_pref[kMaxSeg + 1];
+
+  TileCoord tc;
+  if (!decode_tile<BM, G::OUT_BN, GM>(p, s_pref, tc)) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane >> 3;
+  const long long k0 = static_cast<long long>(tc.split) * p.K;
+
+  const BufRef rA{static_cast<const uint8_t*>(p.a) + k0, p.a_rows_cap * p.lda - k0};
+  uint32_t a_voff[A_PW];
+#pragma unroll
+  for (int i = 0; i < A_PW; ++i) {
+    const int row = (wave * A_PW + i) * 8 + lrow;
+    const int gr = min(tc.row0 + row, tc.row_end - 1);
+    const long long src = p.a_rows ? static_cast<long long>(p.a_rows[gr]) : static_cast<long long>(gr);
+    a_voff[i] = static_cast<uint32_t>(src * p.lda + (((lane & 7) ^ swz(row)) << 4));
+  }
+  const uint8_t* b_base = static_cast<const uint8_t*>(p.b) + static_cast<long long>(tc.expert) * p.b_estride + k0;
+  const BufRef rB{b_base, p.b_estride - k0};
+  uint32_t b_voff[B_PW];
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i) {
+    const int R = (wave * B_PW + i) * 8 + lrow;
+    const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
+    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb + (((lane & 7) ^ swz(R)) << 4));
+  }
+
+  const int wm = wave % WGM;
+  const int wn = wave / WGM;
+  f32x4_t acc[G::MB][G::NB];
+#pragma unroll
+  for (int i = 0; i < G::MB; ++i)
+#pragma unroll
+    for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // The slab DMA helper addresses LDS in bf16 units (512 per 1 KiB block).
+  uint16_t* a0 = reinterpret_cast<uint16_t*>(sA0);
+  uint16_t* a1 = reinterpret_cast<uint16_t*>(sA1);
+  uint16_t* b0 = reinterpret_cast<uint16_t*>(sB0);
+  uint16_t* b1 = reinterpret_cast<uint16_t*>(sB1);
+  const int KT = p.K / BKB;
+  issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, a0, b0, wave, 0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, a1, b1, wave, (kt + 1) * BKB);
+    slab_mma_fp8<G>(acc, sA0, sB0, wm, wn, lane);
+    __syncthreads();
+    if (kt + 2 < KT) issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, a0, b0, wave, (kt + 2) * BKB);
+    slab_mma_fp8<G>(acc, sA1, sB1, wm, wn, lane);
+    __syncthreads();
+  }
+  if (kt < KT) slab_mma_fp8<G>(acc, sA0, sB0, wm, wn, lane);
+  const float* scale = p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows;
+  epilogue<G, EPI>(p, tc, acc, wm, wn, lane, scale);
+}
+
 // ---------------------------------------------------------------------------- fp8 weights (W8A16)
 template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
 __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8w_kernel(GemmArgs p) {
@@ -494,7 +607,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8w_kernel(GemmA
 
 // ---------------------------------------------------------------------------- launch
 template <int BM, int BN, int WGM, int WGN, int EPI, bool BFP8, int GM>
-static hipError_t launch_cfg(const GemmArgs& p, int max_rows, hipStream_t s) {
+static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStream_t s) {
   constexpr int OUT_BN = (EPI == kEpiSiluBF16) ? BN / 2 : BN;
   const int n_tiles = p.N / OUT_BN;
   const long long max_mt = (static_cast<long long>(max_rows) + BM - 1) / BM + p.S;
@@ -503,7 +616,10 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, hipStream_t s) {
   if (grid < kNumXcd) grid = kNumXcd;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
   // A plain runtime branch: both kernels of a configuration are instantiated together.
-  if (BFP8)
+  if (BFP8 && a_fp8)
+    hipLaunchKernelGGL((grouped_gemm_fp8_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
+                       dim3(WGM * WGN * 64), 0, s, p);
+  else if (BFP8)
     hipLaunchKernelGGL((grouped_gemm_fp8w_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
   else
@@ -513,12 +629,12 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, hipStream_t s) {
 }
 
 template <int EPI, bool BFP8>
-static hipError_t launch_epi(const GemmArgs& p, int max_rows, int tile, hipStream_t s) {
+static hipError_t launch_epi(const GemmArgs& p, int max_rows, int tile, bool a_fp8, hipStream_t s) {
   switch (tile) {
-    case kTileL: return launch_cfg<256, 256, 4, 2, EPI, BFP8, 4>(p, max_rows, s);
-    case kTileM: return launch_cfg<128, 128, 2, 2, EPI, BFP8, 4>(p, max_rows, s);
-    case kTileS: return launch_cfg<32, 128, 1, 4, EPI, BFP8, 1>(p, max_rows, s);
-    case kTileXS: return launch_cfg<16, 64, 1, 2, EPI, BFP8, 1>(p, max_rows, s);
+    case kTileL: return launch_cfg<256, 256, 4, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
+    case kTileM: return launch_cfg<128, 128, 2, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
+    case kTileS: return launch_cfg<32, 128, 1, 4, EPI, BFP8, 1>(p, max_rows, a_fp8, s);
+    case kTileXS: return launch_cfg<16, 64, 1, 2, EPI, BFP8, 1>(p, max_rows, a_fp8, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -547,14 +663,16 @@ int gemm_pick_tile(int epi, int max_rows, int S, int N) {
   return t;
 }
 
-hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, int max_rows, int tile, hipStream_t s) {
+hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
+                               hipStream_t s) {
+  if (a_fp8 && !b_fp8) return hipErrorInvalidValue;
   if (tile == kTileAuto) tile = gemm_pick_tile(epi, max_rows, p.S, p.N);
-  if (epi == kEpiSiluBF16) return b_fp8 ? launch_epi<kEpiSiluBF16, true>(p, max_rows, tile, s)
-                                        : launch_epi<kEpiSiluBF16, false>(p, max_rows, tile, s);
-  if (epi == kEpiStoreBF16) return b_fp8 ? launch_epi<kEpiStoreBF16, true>(p, max_rows, tile, s)
-                                         : launch_epi<kEpiStoreBF16, false>(p, max_rows, tile, s);
-  return b_fp8 ? launch_epi<kEpiStoreF32, true>(p, max_rows, tile, s)
-               : launch_epi<kEpiStoreF32, false>(p, max_rows, tile, s);
+  if (epi == kEpiSiluBF16) return b_fp8 ? launch_epi<kEpiSiluBF16, true>(p, max_rows, tile, a_fp8, s)
+                                        : launch_epi<kEpiSiluBF16, false>(p, max_rows, tile, false, s);
+  if (epi == kEpiStoreBF16) return b_fp8 ? launch_epi<kEpiStoreBF16, true>(p, max_rows, tile, a_fp8, s)
+                                         : launch_epi<kEpiStoreBF16, false>(p, max_rows, tile, false, s);
+  return b_fp8 ? launch_epi<kEpiStoreF32, true>(p, max_rows, tile, a_fp8, s)
+               : launch_epi<kEpiStoreF32, false>(p, max_rows, tile, false, s);
 }
 
 }  // namespace eimoe

@@ -33,6 +33,7 @@ struct GemmArgs {
   int k_split;
   int max_rows;              // rows of A (non-gathered) / of C; segment bounds are clamped to it
   long long a_rows_cap;      // rows in the A buffer (bounds the buffer resource)
+  const float* a_scale;      // fp8 A: per-row dequantisation scale, indexed like A (through a_rows)
 };
 
 // Tile shape selector; the launcher maps it to a kernel instantiation.
@@ -50,7 +51,9 @@ hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long spl
                           const float* w, int T, int k, int H, const void* shared_y, int shared_dtype, void* out,
                           int out_dtype, hipStream_t s);
 // epi: Epilogue; b_fp8: B is e4m3; max_rows bounds the grid; tile: TileCfg.
-hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, int max_rows, int tile, hipStream_t s);
+// a_fp8: A and B are both fp8-e4m3 (W8A8 on the fp8 MFMA); b_fp8 alone: W8A16.
+hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
+                               hipStream_t s);
 int gemm_pick_tile(int epi, int max_rows, int S, int N);
 int gemm_out_cols_per_tile(int tile, int epi);
 hipError_t launch_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,

@@ -130,6 +130,44 @@ def gemm_down(h: torch.Tensor, w_down: torch.Tensor, seg_offsets: torch.Tensor, 
     return y
 
 
+def gemm_gate_up_silu_w8a8(aq: torch.Tensor, a_scale: torch.Tensor, w_gate_up: torch.Tensor, w_scale: torch.Tensor,
+                           seg_offsets: torch.Tensor, max_rows: int, a_rows: Optional[torch.Tensor] = None,
+                           e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
+    """W8A8 gate/up: fp8 activations (per-row scales) x fp8 weights (per-channel scales), fp8 MFMA,
+    silu(g)*u -> bf16 [max_rows, I]."""
+    _req(aq, "aq", torch.float8_e4m3fn, 2)
+    _req(a_scale, "a_scale", torch.float32)
+    _req(w_gate_up, "w_gate_up", torch.float8_e4m3fn, 3)
+    _req(w_scale, "w_scale", torch.float32)
+    _req(seg_offsets, "seg_offsets", torch.int32, 1)
+    E, I2, H = w_gate_up.shape
+    I = I2 // 2
+    if a_rows is not None:
+        _req(a_rows, "a_rows", torch.int32)
+    h = torch.empty(max_rows, I, dtype=torch.bfloat16, device=aq.device)
+    call("eimoe_gemm_gate_up_silu_w8a8", aq.data_ptr(), a_scale.data_ptr(), _ptr(a_rows), aq.shape[0], aq.stride(0),
+         w_gate_up.data_ptr(), w_scale.data_ptr(), H, I, seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E,
+         max_rows, h.data_ptr(), tile, _stream(aq))
+    return h
+
+
+def gemm_down_w8a8(hq: torch.Tensor, h_scale: torch.Tensor, w_down: torch.Tensor, w_scale: torch.Tensor,
+                   seg_offsets: torch.Tensor, max_rows: int, out_dtype=torch.float32, k_split: int = 1,
+                   e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
+    """W8A8 down: y = (hq . Wq^T) * h_scale[row] * w_scale[col] -> [k_split, max_rows, H]."""
+    _req(hq, "hq", torch.float8_e4m3fn, 2)
+    _req(h_scale, "h_scale", torch.float32)
+    _req(w_down, "w_down", torch.float8_e4m3fn, 3)
+    _req(w_scale, "w_scale", torch.float32)
+    _req(seg_offsets, "seg_offsets", torch.int32, 1)
+    E, H, I = w_down.shape
+    y = torch.empty(k_split, max_rows, H, dtype=out_dtype, device=hq.device)
+    call("eimoe_gemm_down_w8a8", hq.data_ptr(), h_scale.data_ptr(), I, w_down.data_ptr(), w_scale.data_ptr(), H,
+         seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, y.data_ptr(), _dt(y), k_split, tile,
+         _stream(hq))
+    return y
+
+
 def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg_offsets: torch.Tensor, max_rows: int,
                  out_dtype=torch.bfloat16, a_rows: Optional[torch.Tensor] = None,
                  b_scale: Optional[torch.Tensor] = None, e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
@@ -189,7 +227,7 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
               w_down: torch.Tensor, *, renormalize: bool = True, shared_gate_up: Optional[torch.Tensor] = None,
               shared_down: Optional[torch.Tensor] = None, expert_range: Optional[Sequence[int]] = None,
               w_scales: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, out_dtype=None, y_fp32: bool = False,
-              workspace: Optional[torch.Tensor] = None, return_routing: bool = False):
+              w8a8: bool = False, workspace: Optional[torch.Tensor] = None, return_routing: bool = False):
     """The MoE layer: (hidden_states [T,H], router_logits [T,E], top_k) -> combined output [T,H].
 
     Reproduces MoeAll2AllBlock's stages at ep=1 (moe_all2all.py:85-95) with
@@ -200,7 +238,9 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     ``expert_range=(lo, hi)``: only experts [lo, hi) of the router's E are resident
     (one GPU's EP share); ``w_gate_up``/``w_down`` hold exactly those.  Tokens with
     no resident expert produce zero rows.
-    ``w_scales=(s_gate_up [E,2I], s_down [E,H])`` marks fp8-e4m3 weights (W8A16).
+    ``w_scales=(s_gate_up [E,2I], s_down [E,H])`` marks fp8-e4m3 weights: bf16 activations on
+    the bf16 MFMA (W8A16), or with ``w8a8=True`` activations quantised per token / per row
+    and both GEMMs on the fp8 MFMA (W8A8).
     fp32 hidden states are rounded to bf16 for the MFMA path.
     """
     x = hidden_states
@@ -228,7 +268,9 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
         _req(shared_gate_up, "shared_gate_up", torch.bfloat16, 2)
         _req(shared_down, "shared_down", torch.bfloat16, 2)
         Is = shared_down.shape[1]
-    flags = (_lib.RENORMALIZE if renormalize else 0) | (_lib.Y_F32 if y_fp32 else 0)
+    if w8a8 and not fp8:
+        raise ValueError("w8a8 needs fp8 weights and w_scales")
+    flags = (_lib.RENORMALIZE if renormalize else 0) | (_lib.Y_F32 if y_fp32 else 0) | (_lib.W8A8 if w8a8 else 0)
     need = fused_moe_workspace_bytes(T, H, I, E, top_k, n_local, Is, out_dtype, flags)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)

@@ -44,7 +44,8 @@ enum { EIMOE_F32 = 0, EIMOE_BF16 = 1, EIMOE_FP8 = 2 };
 /* flags for eimoe_fused_moe */
 enum {
   EIMOE_RENORMALIZE = 1, /* renormalise the top-k weights (norm_topk_prob) */
-  EIMOE_Y_F32 = 2        /* keep the per-assignment expert outputs in fp32 (default: output dtype) */
+  EIMOE_Y_F32 = 2,       /* keep the per-assignment expert outputs in fp32 (default: output dtype) */
+  EIMOE_W8A8 = 4         /* fp8 weights: also quantise activations per token and run the fp8 MFMA */
 };
 
 /* tile selector for the GEMM entry points (0 = automatic) */
@@ -106,6 +107,21 @@ int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int a_nrows, i
 int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const float* w_scale, int H,
                     const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows, void* y, int y_dtype,
                     int k_split, int tile, void* stream);
+
+/* W8A8 twins of the two expert GEMMs: fp8-e4m3 activations with per-row scales and fp8-e4m3
+ * weights with per-output-channel scales, on the gfx950 fp8 MFMA; result = acc * a_scale[row] *
+ * w_scale[col] (the gate/up pair scaled before SiLU*mul).  No reference counterpart
+ * (fused_moe.py:331-335 maps fp8 inputs to a bf16 compute type and takes no scales).
+ * gate/up: a [a_nrows, lda] fp8, a_scale[a_nrows] (row r uses a_scale[a_rows ? a_rows[r] : r]);
+ *          H % 128 == 0, I % 32 == 0; h bf16 [max_rows, I].
+ * down:    hq [max_rows, I] fp8, h_scale[max_rows]; I/k_split % 128 == 0. */
+int eimoe_gemm_gate_up_silu_w8a8(const void* a, const float* a_scale, const int32_t* a_rows, int a_nrows, int lda,
+                                 const void* w_gate_up, const float* w_scale, int H, int I,
+                                 const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows, void* h, int tile,
+                                 void* stream);
+int eimoe_gemm_down_w8a8(const void* hq, const float* h_scale, int I, const void* w_down, const float* w_scale, int H,
+                         const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows, void* y, int y_dtype,
+                         int k_split, int tile, void* stream);
 
 /* Plain grouped GEMM, the X_grouped_gemm_single(A, B_list, block_sizes) contract
  * (single_group_gemm_moe.py:76-91): c[rows_s] = a[rows_s] . B[s % e_mod]^T with B packed as

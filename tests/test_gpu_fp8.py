@@ -1,0 +1,128 @@
+"""fp8 paths on the GPU.
+
+W8A8 (fp8 activations and weights on the fp8 MFMA): each GEMM is compared with the
+oracle on the same quantised operands (tight: only fp32 accumulation order and
+bf16 storage of h differ), and the layer with the oracle's W8A8 forward.  Against
+the bf16 fp32 reference the W8A8 layer carries e4m3 rounding of both operands of
+both GEMMs (~6.5% rel-L2 on N(0,0.02) weights), which is reported, not asserted
+at 5e-2; the W8A16 layer meets 5e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from easyinfra_amd import ops
+from easyinfra_amd.workloads import SHAPES, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def cpu(t):
+    return t.detach().cpu()
+
+
+def _segments(counts):
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    return off, torch.as_tensor(off)
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+def test_w8a8_gate_up_matches_oracle(dev, tile):
+    g = torch.Generator().manual_seed(tile)
+    H, I, T = 256, 256, 50
+    counts = [0, 37, 300, 5]
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
+    w = torch.randn(E, 2 * I, H, generator=g) * 0.02
+    qw, sw = oracle.quantize_weights_fp8(w)
+    xq, sx = oracle.quantize_rows_fp8(x)
+    h = ops.gemm_gate_up_silu_w8a8(xq.to(dev), sx.to(dev), qw.to(dev), sw.to(dev), off_t.to(dev), rows,
+                                   a_rows=a_rows.to(dev), tile=tile)
+    h = cpu(h).float()
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        tok = a_rows[a:b].long()
+        gu = (xq[tok].float() @ qw[e].float().T) * sx[tok][:, None] * sw[e][None, :]
+        ref = oracle.silu(gu[:, :I]) * gu[:, I:]
+        torch.testing.assert_close(h[a:b], ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 2), (4, 1)])
+def test_w8a8_down_matches_oracle(dev, tile, k_split):
+    g = torch.Generator().manual_seed(10 + tile)
+    H, I = 256, 512
+    counts = [3, 0, 260, 41]
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    h = torch.randn(rows, I, generator=g) * 0.5
+    hq, sh = oracle.quantize_rows_fp8(h)
+    w = torch.randn(E, H, I, generator=g) * 0.02
+    qw, sw = oracle.quantize_weights_fp8(w)
+    y = ops.gemm_down_w8a8(hq.to(dev), sh.to(dev), qw.to(dev), sw.to(dev), off_t.to(dev), rows, k_split=k_split,
+                           tile=tile)
+    y = cpu(y).sum(0)
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        ref = (hq[a:b].float() @ qw[e].float().T) * sh[a:b][:, None] * sw[e][None, :]
+        torch.testing.assert_close(y[a:b], ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("name,T", [("mixtral-8x7b-fp8", 96), ("mixtral-8x7b-fp8", 7), ("qwen3-30b-a3b-local32", 64)])
+def test_w8a8_layer(dev, name, T):
+    inp = make_inputs(SHAPES[name], T, device="cpu", hidden=256, inter=256)
+    s = inp.shape
+    qgu, sgu = oracle.quantize_weights_fp8(inp.w_gate_up.float())
+    qd, sd = oracle.quantize_weights_fp8(inp.w_down.float())
+    out = ops.fused_moe(inp.x.to(dev), inp.logits.to(dev), s.top_k, qgu.to(dev), qd.to(dev),
+                        renormalize=s.renormalize, expert_range=inp.expert_range,
+                        w_scales=(sgu.to(dev), sd.to(dev)), out_dtype=torch.float32, w8a8=True)
+    got = cpu(out)
+    ref8 = oracle.moe_forward_fp8(inp.x, inp.logits, s.top_k, qgu, sgu, qd, sd, s.renormalize, mode="w8a8",
+                                  expert_range=inp.expert_range)
+    ref = oracle.moe_forward(inp.x, inp.logits, s.top_k, inp.w_gate_up, inp.w_down, s.renormalize,
+                             expert_range=inp.expert_range)
+    # h is quantised from its bf16 copy on the GPU and from fp32 in the oracle: a few e4m3
+    # values round differently, hence a looser bound than the GEMM checks above.
+    assert oracle.rel_l2(got, ref8) <= 3e-2
+    print(f"{name} T={T}: W8A8 vs W8A8-oracle {oracle.rel_l2(got, ref8):.3e}, vs bf16-ref {oracle.rel_l2(got, ref):.3e}")
+    assert oracle.rel_l2(got, ref) <= 1e-1
+
+
+def test_w8a16_layer_meets_fp8_tolerance(dev):
+    inp = make_inputs(SHAPES["mixtral-8x7b-fp8"], 96, device="cpu", hidden=256, inter=256)
+    qgu, sgu = oracle.quantize_weights_fp8(inp.w_gate_up.float())
+    qd, sd = oracle.quantize_weights_fp8(inp.w_down.float())
+    out = ops.fused_moe(inp.x.to(dev), inp.logits.to(dev), 2, qgu.to(dev), qd.to(dev),
+                        w_scales=(sgu.to(dev), sd.to(dev)), out_dtype=torch.float32)
+    ref = oracle.moe_forward(inp.x, inp.logits, 2, inp.w_gate_up, inp.w_down, True)
+    ref16 = oracle.moe_forward_fp8(inp.x, inp.logits, 2, qgu, sgu, qd, sd, True, mode="w8a16")
+    assert oracle.rel_l2(cpu(out), ref16) <= 1e-2
+    assert oracle.rel_l2(cpu(out), ref) <= 5e-2
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("T", [64, 8192])
+def test_fp8_mixtral_real_shape(dev, T):
+    """Mixtral-8x7B with fp8-e4m3 weights (per-channel absmax/448) against the bf16 fp32 reference."""
+    inp = make_inputs(SHAPES["mixtral-8x7b-fp8"], T, device=dev)
+    s = inp.shape
+    qgu, sgu = ops.quantize_weights_fp8(inp.w_gate_up)
+    qd, sd = ops.quantize_weights_fp8(inp.w_down)
+    sub = torch.randperm(T, generator=torch.Generator().manual_seed(T))[:16]
+    ref = oracle.moe_forward(cpu(inp.x), cpu(inp.logits), 2, cpu(inp.w_gate_up), cpu(inp.w_down), True,
+                             token_subset=sub)
+    res = {}
+    for mode in ("w8a16", "w8a8"):
+        out = ops.fused_moe(inp.x, inp.logits, 2, qgu, qd, w_scales=(sgu, sd), out_dtype=torch.float32,
+                            w8a8=(mode == "w8a8"))
+        res[mode] = oracle.rel_l2(cpu(out)[sub], ref)
+    print(f"fp8 mixtral T={T}: rel-L2 vs bf16 reference {res}")
+    assert res["w8a16"] <= 5e-2
+    assert res["w8a8"] <= 1e-1
