@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--decode-tokens", type=int, default=64)
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="token sample for the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--traffic-run", action="store_true",
+                    help="counter-collection driver: a 1 GiB device copy (known bytes, calibrates FETCH_SIZE/"
+                         "WRITE_SIZE) followed by two fused prefill layers; prints no JSON line")
     return ap.parse_args()
 
 
@@ -129,13 +132,30 @@ def cpu_baseline(inp, n_tokens, runs, torch):
 
 
 def traffic_from_profiles(kernel_tag):
+    """HBM bytes per launch of one kernel, from counter runs of ``--traffic-run``
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for the 1 GiB copy)."""
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
         return None
     try:
-        return json.loads(f.read_text()).get(kernel_tag)
-    except (ValueError, OSError):
+        rec = json.loads(f.read_text()).get(kernel_tag)
+        return None if rec is None else int(rec["traffic_bytes"])
+    except (ValueError, OSError, KeyError, TypeError):
         return None
+
+
+def traffic_run(torch, ops, shape, make_inputs, tokens):
+    src = torch.empty(512 << 20, dtype=torch.bfloat16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)                       # 1 GiB read + 1 GiB written
+    torch.cuda.synchronize()
+    del src, dst
+    inp = make_inputs(shape, tokens, device="cuda")
+    for _ in range(2):
+        ops.fused_moe(inp.x, inp.logits, shape.top_k, inp.w_gate_up, inp.w_down, renormalize=shape.renormalize)
+    torch.cuda.synchronize()
+    print("traffic run done", flush=True)
 
 
 def main():
@@ -151,6 +171,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     shape = MIXTRAL_8X7B
+    if args.traffic_run:
+        traffic_run(torch, ops, shape, make_inputs, args.tokens)
+        return
     T = args.tokens
     inp = make_inputs(shape, T, device=dev)
     H, I, k = shape.hidden, shape.inter, shape.top_k
@@ -169,7 +192,7 @@ def main():
     gu_flops = 4.0 * A * H * I
     gu_ms = stages["gate_up_silu"]
     achieved = gu_flops / (gu_ms * 1e-3) / 1e12
-    roof = {"bound": "mfma", "kernel": "grouped_gemm_kernel<256,256,...,silu> (gate/up + SiLU*mul)",
+    roof = {"bound": "mfma", "kernel": "grouped_gemm_dma_kernel<256,256,4,2,2,4> (gate/up + SiLU*mul)",
             "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic_from_profiles("gate_up_silu_prefill"),
             "flops_per_launch": gu_flops, "mean_launch_ms": round(gu_ms, 4)}
