@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--decode-tokens", type=int, default=64)
-    ap.add_argument("--cpu-tokens", type=int, default=1024, help="token sample for the CPU baseline (0 = skip)")
+    ap.add_argument("--cpu-tokens", type=int, default=8192, help="token sample for the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-runs", type=int, default=3)
     ap.add_argument("--traffic-run", action="store_true",
                     help="counter-collection driver: a 1 GiB device copy (known bytes, calibrates FETCH_SIZE/"

@@ -282,6 +282,15 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
 
 // Issues one K slab of A and B straight into LDS: each wave instruction fills one
 // contiguous 1 KiB block (16 bytes per lane).
+// Keeps the next slab's loads at the top of the current slab's MFMA work.  Without it the
+// machine scheduler sinks them towards the barrier, whose vmcnt(0) then exposes their whole
+// latency on every other slab.
+__device__ __forceinline__ void pin_issue() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_sched_barrier(0);
+#endif
+}
+
 template <int A_PW, int B_PW>
 __device__ __forceinline__ void issue_slab_dma(const BufRef& a, const BufRef& b, const uint32_t (&a_voff)[A_PW],
                                                const uint32_t (&b_voff)[B_PW], uint16_t* sA, uint16_t* sB, int wave,
@@ -403,11 +412,17 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
   issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, 0);
   __syncthreads();
   int kt = 0;
-  for (; kt + 1 < KT; kt += 2) {   // stage kt is in buffer 0 here
+  // Slab kt is in buffer 0 at the top of each iteration.  The second load is unconditional
+  // (on the last iteration of an even slab count it re-reads slab KT-1 into buffer 0, which is
+  // not read again and which the closing barrier waits for) so that it is not split into its
+  // own basic block, where the scheduler would queue the previous slab's MFMAs ahead of it.
+  for (; kt + 1 < KT; kt += 2) {
     issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA1, sB1, wave, (kt + 1) * BK * 2);
+    pin_issue();
     slab_mma<G>(acc, sA0, sB0, wm, wn, lane);
     __syncthreads();
-    if (kt + 2 < KT) issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, (kt + 2) * BK * 2);
+    issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, min(kt + 2, KT - 1) * BK * 2);
+    pin_issue();
     slab_mma<G>(acc, sA1, sB1, wm, wn, lane);
     __syncthreads();
   }
@@ -515,9 +530,11 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8_kernel(GemmAr
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
     issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, a1, b1, wave, (kt + 1) * BKB);
+    pin_issue();
     slab_mma_fp8<G>(acc, sA0, sB0, wm, wn, lane);
     __syncthreads();
-    if (kt + 2 < KT) issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, a0, b0, wave, (kt + 2) * BKB);
+    issue_slab_dma<A_PW, B_PW>(rA, rB, a_voff, b_voff, a0, b0, wave, min(kt + 2, KT - 1) * BKB);
+    pin_issue();
     slab_mma_fp8<G>(acc, sA1, sB1, wm, wn, lane);
     __syncthreads();
   }
