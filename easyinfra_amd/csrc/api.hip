@@ -58,15 +58,36 @@ int check_tile(int tile, int epi, int N) {
   return EIMOE_OK;
 }
 
-// Split of the down projection's K so that small (decode) launches still fill the GPU.
-int pick_down_split(int max_rows, int n_local, int H, int I) {
+// Split of the down projection's K.  Work items (m-tiles x n-tiles x split) run in rounds
+// of kNumCu workgroups, so a launch whose tile count sits just past a multiple of kNumCu
+// wastes most of its last round (the Mixtral prefill layer: ~1104 tiles = 4.3 rounds).
+// Each candidate split is charged its padded rounds, in units of one full-K tile, plus the
+// HBM round trip of its extra partial planes (written here, read back by the combine);
+// small launches also split until they fill the GPU twice over.
+int pick_down_split(int max_rows, int n_local, int H, int I, int y_elem) {
   const int tile = gemm_pick_tile(kEpiStoreF32, max_rows, n_local, H);
   const int bm = tile == kTileL ? 256 : tile == kTileM ? 128 : tile == kTileS ? 32 : 16;
-  const long long mt = std::min<long long>(n_local, max_rows) + max_rows / bm;
-  const long long tiles = mt * (H / gemm_out_cols_per_tile(tile, kEpiStoreF32));
-  int split = 1;
-  while (split < 8 && tiles * split < 2 * kNumCu && (I % (64 * split * 2)) == 0) split *= 2;
-  return split;
+  const int bn = gemm_out_cols_per_tile(tile, kEpiStoreF32);
+  const long long mt = std::min<long long>(n_local, max_rows) + max_rows / bm;   // bound on m-tiles
+  const long long tiles = mt * (H / bn);
+  constexpr double kTileFlops = 4.7e12;   // measured bf16 GEMM rate per CU, FLOP/s
+  constexpr double kHbm = 5.0e12;         // achieved HBM rate for plane traffic, B/s
+  const double t_tile = 2.0 * bm * bn * static_cast<double>(I) / kTileFlops;
+  const double t_plane = 2.0 * static_cast<double>(max_rows) * H * y_elem / kHbm;
+  int best = 1;
+  double best_cost = 1e300;
+  for (int split = 1; split <= 8; split *= 2) {
+    if (I % (64 * split) != 0) break;
+    const long long items = tiles * split;
+    const long long rounds = (items + kNumCu - 1) / kNumCu;
+    double cost = static_cast<double>(rounds) / split * t_tile + (split - 1) * t_plane;
+    if (items < 2 * kNumCu && split < 8 && I % (128 * split) == 0) cost = 1e300;   // too few to fill the GPU
+    if (cost < best_cost * 0.98) {
+      best_cost = cost;
+      best = split;
+    }
+  }
+  return best;
 }
 
 struct FusedLayout {
@@ -79,7 +100,9 @@ FusedLayout fused_layout(int T, int H, int I, int k, int n_local, int Is, int ou
   FusedLayout L{};
   const size_t A = static_cast<size_t>(T) * k;
   L.y_dtype = ((flags & EIMOE_Y_F32) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
-  L.k_split = pick_down_split(static_cast<int>(A), n_local, H, (flags & EIMOE_W8A8) ? I / 2 : I);
+  // W8A8 planes cover K slices that are multiples of 128: pick the split on I/2 in 64s.
+  L.k_split = pick_down_split(static_cast<int>(A), n_local, H, (flags & EIMOE_W8A8) ? I / 2 : I,
+                              static_cast<int>(elem_size(L.y_dtype)));
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
