@@ -50,7 +50,7 @@ int check_gemm_common(int max_rows, int n_seg, int e_mod) {
 }
 
 int check_tile(int tile, int epi, int N) {
-  if (tile < EIMOE_TILE_AUTO || tile > EIMOE_TILE_16x64) return fail(EIMOE_ERR_SHAPE, "tile=%d unknown", tile);
+  if (tile < EIMOE_TILE_AUTO || tile > EIMOE_TILE_STREAM) return fail(EIMOE_ERR_SHAPE, "tile=%d unknown", tile);
   if (tile != EIMOE_TILE_AUTO) {
     const int oc = gemm_out_cols_per_tile(tile, epi);
     if (N % oc != 0) return fail(EIMOE_ERR_ALIGN, "N=%d not a multiple of the tile's %d output columns", N, oc);
@@ -66,6 +66,16 @@ int check_tile(int tile, int epi, int N) {
 // small launches also split until they fill the GPU twice over.
 int pick_down_split(int max_rows, int n_local, int H, int I, int y_elem) {
   const int tile = gemm_pick_tile(kEpiStoreF32, max_rows, n_local, H);
+  if (tile == kTileXS) {
+    // Few rows per segment: the weight-streaming kernel (bf16 weights) runs one 4-wave
+    // workgroup per (segment, column group, 32-row chunk, split).  Split until there are
+    // about 6 workgroups per CU, keeping K/64 per split a multiple of 8 (4 waves x 2 steps).
+    const int cols = std::max(stream_out_cols(H, kEpiStoreF32), 16);
+    const long long tasks = (std::min<long long>(n_local, max_rows) + (max_rows + 31) / 32) * (H / cols);
+    int split = 1;
+    while (split < 8 && tasks * split < 6ll * kNumCu && I % (64 * 8 * split * 2) == 0) split *= 2;
+    return split;
+  }
   const int bm = tile == kTileL ? 256 : tile == kTileM ? 128 : tile == kTileS ? 32 : 16;
   const int bn = gemm_out_cols_per_tile(tile, kEpiStoreF32);
   const long long mt = std::min<long long>(n_local, max_rows) + max_rows / bm;   // bound on m-tiles

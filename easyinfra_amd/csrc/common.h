@@ -52,6 +52,14 @@ __device__ __forceinline__ float silu_f32(float g) {
   return g / (1.0f + __expf(-g));
 }
 
+// Raw buffer resource over [base, base + bytes): loads past the end return zero.
+constexpr int kBufDword3 = 0x00020000;  // gfx9 raw buffer resource word 3
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long long bytes) {
+  const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0xffffffffll ? 0xffffffffu : static_cast<uint32_t>(bytes));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(n),
+                                           kBufDword3);
+}
+
 // Wave-wide inclusive prefix sum (64 lanes).
 __device__ __forceinline__ int wave_incl_scan(int v) {
   const int lane = threadIdx.x & 63;

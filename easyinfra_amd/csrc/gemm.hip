@@ -35,14 +35,7 @@
 
 namespace eimoe {
 
-constexpr int kBufDword3 = 0x00020000;  // gfx9 raw buffer resource word 3
 typedef __attribute__((address_space(3))) void lds_void_t;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long long bytes) {
-  const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0xffffffffll ? 0xffffffffu : static_cast<uint32_t>(bytes));
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(n),
-                                           kBufDword3);
-}
 
 // A buffer window: base address and byte size (bounds the hardware buffer resource).
 struct BufRef {
@@ -657,6 +650,7 @@ static hipError_t launch_epi(const GemmArgs& p, int max_rows, int tile, bool a_f
 }
 
 int gemm_out_cols_per_tile(int tile, int epi) {
+  if (tile == kTileStream) return epi == kEpiSiluBF16 ? 16 : 32;   // narrowest task; wider when N allows
   int bn = 0;
   switch (tile) {
     case kTileL: bn = 256; break;
@@ -683,7 +677,16 @@ int gemm_pick_tile(int epi, int max_rows, int S, int N) {
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
                                hipStream_t s) {
   if (a_fp8 && !b_fp8) return hipErrorInvalidValue;
-  if (tile == kTileAuto) tile = gemm_pick_tile(epi, max_rows, p.S, p.N);
+  if (tile == kTileAuto) {
+    tile = gemm_pick_tile(epi, max_rows, p.S, p.N);
+    // a few rows per segment: stream the bf16 weights instead of tiling them through LDS
+    if (tile == kTileXS && !b_fp8 && stream_gemm_supported(p, epi)) tile = kTileStream;
+  }
+  if (tile == kTileStream) {
+    if (b_fp8 || !stream_gemm_supported(p, epi)) return hipErrorInvalidValue;
+    const double avg = static_cast<double>(max_rows) / (p.S > 0 ? p.S : 1);
+    return launch_stream_gemm(p, epi, max_rows, avg > 8 ? 2 : 1, s);
+  }
   if (epi == kEpiSiluBF16) return b_fp8 ? launch_epi<kEpiSiluBF16, true>(p, max_rows, tile, a_fp8, s)
                                         : launch_epi<kEpiSiluBF16, false>(p, max_rows, tile, false, s);
   if (epi == kEpiStoreBF16) return b_fp8 ? launch_epi<kEpiStoreBF16, true>(p, max_rows, tile, a_fp8, s)

@@ -37,7 +37,7 @@ struct GemmArgs {
 };
 
 // Tile shape selector; the launcher maps it to a kernel instantiation.
-enum TileCfg : int { kTileAuto = 0, kTileL = 1, kTileM = 2, kTileS = 3, kTileXS = 4 };
+enum TileCfg : int { kTileAuto = 0, kTileL = 1, kTileM = 2, kTileS = 3, kTileXS = 4, kTileStream = 5 };
 
 hipError_t launch_router_topk(const float* logits, int T, int E, int k, int renorm, int32_t* ids, float* w,
                               hipStream_t s);
@@ -55,6 +55,10 @@ hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long spl
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
                                hipStream_t s);
 int gemm_pick_tile(int epi, int max_rows, int S, int N);
+// Weight-streaming kernel (stream.hip) for segments of a few rows; bf16 weights only.
+bool stream_gemm_supported(const GemmArgs& p, int epi);
+int stream_out_cols(int N, int epi);   // output columns per streaming task (0: unsupported)
+hipError_t launch_stream_gemm(const GemmArgs& p, int epi, int max_rows, int mblk, hipStream_t s);
 int gemm_out_cols_per_tile(int tile, int epi);
 hipError_t launch_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,
                                     hipStream_t s);

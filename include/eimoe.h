@@ -48,9 +48,12 @@ enum {
   EIMOE_W8A8 = 4         /* fp8 weights: also quantise activations per token and run the fp8 MFMA */
 };
 
-/* tile selector for the GEMM entry points (0 = automatic) */
+/* tile selector for the GEMM entry points (0 = automatic).  EIMOE_TILE_STREAM is the
+ * weight-streaming kernel for a few rows per segment (bf16 weights only; K % 64 == 0 and the
+ * output columns a multiple of 16 for gate/up, 32 otherwise); automatic selection uses it
+ * for bf16 weights when the average rows per segment are below 24. */
 enum { EIMOE_TILE_AUTO = 0, EIMOE_TILE_256x256 = 1, EIMOE_TILE_128x128 = 2, EIMOE_TILE_32x128 = 3,
-       EIMOE_TILE_16x64 = 4 };
+       EIMOE_TILE_16x64 = 4, EIMOE_TILE_STREAM = 5 };
 
 #define EIMOE_MAX_TOPK 32
 #define EIMOE_MAX_EXPERTS 512

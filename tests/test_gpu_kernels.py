@@ -135,7 +135,7 @@ def _segments(counts):
     return off, torch.as_tensor(off)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("counts", [[0, 5, 300, 1, 64], [17], [0, 0, 3]])
 def test_gate_up_silu(dev, tile, counts):
     g = torch.Generator().manual_seed(sum(counts) + tile)
@@ -159,7 +159,7 @@ def test_gate_up_silu(dev, tile, counts):
         torch.testing.assert_close(h[a:b], ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 4)])
+@pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 4), (5, 1), (5, 2), (5, 8)])
 def test_down_gemm(dev, tile, k_split):
     g = torch.Generator().manual_seed(31 + tile * 7 + k_split)
     H, I = 256, 512
@@ -175,6 +175,37 @@ def test_down_gemm(dev, tile, k_split):
         a, b = int(off[e]), int(off[e + 1])
         ref = h[a:b].float() @ w[e].float().T
         torch.testing.assert_close(y[a:b], ref, rtol=1e-4, atol=1e-4)
+
+
+# The weight-streaming kernel (tile 5) picks its column width (8/4/2 fragments), its K split
+# over 4 waves (when K/64 is a multiple of 4) and its register ring depth (2 or 1) from the
+# shapes; these cases reach every combination, rows past 32 per segment (several row chunks),
+# empty and one-row segments.  Nd is the down projection's output width (0: not run).
+@pytest.mark.parametrize("H,I,Nd", [(256, 256, 256), (192, 32, 0), (512, 96, 0), (64, 32, 0), (1408, 128, 1408),
+                                    (128, 320, 64), (256, 512, 192)])
+def test_stream_gemms_shapes(dev, H, I, Nd):
+    g = torch.Generator().manual_seed(H + I + Nd)
+    counts = [1, 0, 40, 7, 70]
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 50
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16)
+    h = ops.gemm_gate_up_silu(x.to(dev), wgu.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev), tile=5)
+    if Nd:
+        wd = (torch.randn(E, Nd, I, generator=g) * 0.05).to(torch.bfloat16)
+        y = cpu(ops.gemm_down(h, wd.to(dev), off_t.to(dev), rows, out_dtype=torch.float32, tile=5)).sum(0)
+    h = cpu(h).float()
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        gu = x[a_rows[a:b].long()].float() @ wgu[e].float().T
+        torch.testing.assert_close(h[a:b], oracle.silu(gu[:, :I]) * gu[:, I:], rtol=1e-2, atol=1e-2)
+        if Nd:
+            torch.testing.assert_close(y[a:b], h[a:b] @ wd[e].float().T, rtol=1e-4, atol=1e-4)
 
 
 def test_grouped_gemm_single_contract(dev):
