@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--decode-tokens", type=int, default=64)
     ap.add_argument("--cpu-tokens", type=int, default=8192, help="token sample for the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--no-suite", action="store_true",
+                    help="skip the other workloads (tiny fp32 layer, DeepSeek-V2-Lite, Qwen3-30B-A3B local share, "
+                         "fp8 Mixtral)")
     ap.add_argument("--traffic-run", action="store_true",
                     help="counter-collection driver: a 1 GiB device copy (known bytes, calibrates FETCH_SIZE/"
                          "WRITE_SIZE) followed by two fused prefill layers; prints no JSON line")
@@ -158,6 +161,94 @@ def traffic_run(torch, ops, shape, make_inputs, tokens):
     print("traffic run done", flush=True)
 
 
+def timed_cold(fn, steps, warmup, torch, flush):
+    """Mean ms of fn with the device caches flushed before every call (each call bracketed by
+    HIP events on the launch stream, the flush outside them): weights of a small layer would
+    otherwise be served from the 256 MB last-level cache after the first call.  The flush
+    reads a 512 MB buffer (a write would leave dirty lines whose write-back overlaps fn)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        flush.sum()
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / steps
+
+
+def layer_case(name, inp, torch, ops, steps, warmup, flush, *, w8a8=False, fp8w=None):
+    """One fused-layer workload: warm and cache-cold times, tokens/s, TFLOP/s and HBM GB/s."""
+    from easyinfra_amd.workloads import layer_flops, layer_bytes
+    s = inp.shape
+    T, H = inp.x.shape
+    I = s.inter
+    n_local = inp.w_gate_up.shape[0]
+    wgu, wd, scales = inp.w_gate_up, inp.w_down, None
+    if fp8w is not None:
+        wgu, wd, scales = fp8w
+    Is = inp.shared_down.shape[1] if inp.shared_down is not None else 0
+    kw = dict(renormalize=s.renormalize, shared_gate_up=inp.shared_gate_up, shared_down=inp.shared_down,
+              expert_range=inp.expert_range, w_scales=scales, w8a8=w8a8)
+    ws = torch.empty(ops.fused_moe_workspace_bytes(T, H, I, s.n_experts, s.top_k, n_local, Is,
+                                                   flags=4 if w8a8 else 0), dtype=torch.uint8, device=inp.x.device)
+    fn = lambda: ops.fused_moe(inp.x, inp.logits, s.top_k, wgu, wd, workspace=ws, **kw)
+    _, ids, _ = ops.fused_moe(inp.x, inp.logits, s.top_k, wgu, wd, return_routing=True, **kw)
+    lo, hi = inp.expert_range or (0, s.n_experts)
+    local = ids[(ids >= lo) & (ids < hi)]
+    A = int(local.numel())
+    touched = int(torch.unique(local).numel())
+    ms = timed(fn, steps, warmup, torch)
+    ms_cold = timed_cold(fn, steps, 1, torch, flush)
+    flops = layer_flops(A, T, H, I, Is)
+    b_w = 1 if fp8w is not None else 2
+    nbytes = layer_bytes(touched, T, s.n_experts, H, I, b_w, 2, 2, Is, fp8_scales=fp8w is not None)
+    peak = FP8_PEAK_TFLOPS if w8a8 else BF16_PEAK_TFLOPS
+    return {"case": name, "tokens": T, "assignments": A, "touched_experts": touched, "ms": round(ms, 4),
+            "ms_cold": round(ms_cold, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / peak, 4),
+            "hbm_GBps_cold": round(nbytes / (ms_cold * 1e-3) / 1e9, 1),
+            "hbm_frac_cold": round(nbytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def suite(torch, ops, mix_inp, steps, warmup):
+    """The other workloads of the layer, one GPU each: timings only (parity is in tests/)."""
+    from easyinfra_amd.workloads import SHAPES, make_inputs
+    dev = mix_inp.x.device
+    flush = torch.ones(128 << 20, dtype=torch.float32, device=dev)   # 512 MB > the 256 MB last-level cache
+    out = []
+    inp = make_inputs(SHAPES["tiny-mixtral-fp32"], 512, device=dev)
+    inp.w_gate_up, inp.w_down = inp.w_gate_up.to(torch.bfloat16), inp.w_down.to(torch.bfloat16)
+    out.append(layer_case("tiny-mixtral-fp32 T=512 (bf16 MFMA)", inp, torch, ops, steps, warmup, flush))
+    del inp
+    ds = SHAPES["deepseek-v2-lite"]
+    skew = layer_case("deepseek-v2-lite T=4096 zipf(1.2) + 2 shared", make_inputs(ds, 4096, device=dev), torch, ops,
+                      steps, warmup, flush)
+    uni = layer_case("deepseek-v2-lite T=4096 uniform twin", make_inputs(ds, 4096, device=dev, uniform_twin=True),
+                     torch, ops, steps, warmup, flush)
+    skew["skew_over_uniform"] = round(skew["ms"] / uni["ms"], 3)
+    out += [skew, uni]
+    qw = SHAPES["qwen3-30b-a3b-local32"]
+    for T in (1, 32, 256, 2048):
+        hot = layer_case(f"qwen3-30b-a3b local 32/128 T={T} hot:cold 8:1", make_inputs(qw, T, device=dev), torch, ops,
+                         steps, warmup, flush)
+        twin = layer_case(f"qwen3-30b-a3b local 32/128 T={T} uniform twin",
+                          make_inputs(qw, T, device=dev, uniform_twin=True), torch, ops, steps, warmup, flush)
+        hot["skew_over_uniform_cold"] = round(hot["ms_cold"] / twin["ms_cold"], 3)
+        out += [hot, twin]
+    qgu, sgu = ops.quantize_weights_fp8(mix_inp.w_gate_up)
+    qd, sd = ops.quantize_weights_fp8(mix_inp.w_down)
+    for T in (8192, 64):
+        sub = mix_inp if T == mix_inp.x.shape[0] else type(mix_inp)(mix_inp.shape, mix_inp.x[:T].contiguous(),
+                                                                     mix_inp.logits[:T].contiguous(),
+                                                                     mix_inp.w_gate_up, mix_inp.w_down)
+        out.append(layer_case(f"mixtral-8x7b fp8-e4m3 W8A8 T={T}", sub, torch, ops, steps, warmup, flush, w8a8=True,
+                              fp8w=(qgu, qd, (sgu, sd))))
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -211,6 +302,8 @@ def main():
               "hbm_GBps": round(dbytes / (dms * 1e-3) / 1e9, 1),
               "hbm_frac": round(dbytes / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "touched_experts": touched}
 
+    cases = None if args.no_suite else suite(torch, ops, inp, max(5, args.steps // 2), 2)
+
     cpu = None
     if args.cpu_tokens > 0:
         cpu = cpu_baseline(inp, args.cpu_tokens, args.cpu_runs, torch)
@@ -230,6 +323,7 @@ def main():
         "cpu_baseline": cpu,
         "decode": decode,
         "kernels_ms": {k_: round(v, 4) for k_, v in stages.items()},
+        "suite": cases,
     }
     print(json.dumps(line), flush=True)
 

@@ -677,15 +677,18 @@ int gemm_pick_tile(int epi, int max_rows, int S, int N) {
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
                                hipStream_t s) {
   if (a_fp8 && !b_fp8) return hipErrorInvalidValue;
+  // The streaming kernel takes bf16 x bf16 or e4m3 x e4m3; fp8 weights with bf16
+  // activations (W8A16) stay on the LDS-tiled kernels.
+  const bool stream_ok = (b_fp8 == a_fp8) && stream_gemm_supported(p, epi, a_fp8);
   if (tile == kTileAuto) {
     tile = gemm_pick_tile(epi, max_rows, p.S, p.N);
-    // a few rows per segment: stream the bf16 weights instead of tiling them through LDS
-    if (tile == kTileXS && !b_fp8 && stream_gemm_supported(p, epi)) tile = kTileStream;
+    // a few rows per segment: stream the weights instead of tiling them through LDS
+    if (tile == kTileXS && stream_ok) tile = kTileStream;
   }
   if (tile == kTileStream) {
-    if (b_fp8 || !stream_gemm_supported(p, epi)) return hipErrorInvalidValue;
+    if (!stream_ok) return hipErrorInvalidValue;
     const double avg = static_cast<double>(max_rows) / (p.S > 0 ? p.S : 1);
-    return launch_stream_gemm(p, epi, max_rows, avg > 8 ? 2 : 1, s);
+    return launch_stream_gemm(p, epi, a_fp8, max_rows, avg > 8 ? 2 : 1, s);
   }
   if (epi == kEpiSiluBF16) return b_fp8 ? launch_epi<kEpiSiluBF16, true>(p, max_rows, tile, a_fp8, s)
                                         : launch_epi<kEpiSiluBF16, false>(p, max_rows, tile, false, s);

@@ -55,10 +55,11 @@ hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long spl
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
                                hipStream_t s);
 int gemm_pick_tile(int epi, int max_rows, int S, int N);
-// Weight-streaming kernel (stream.hip) for segments of a few rows; bf16 weights only.
-bool stream_gemm_supported(const GemmArgs& p, int epi);
-int stream_out_cols(int N, int epi);   // output columns per streaming task (0: unsupported)
-hipError_t launch_stream_gemm(const GemmArgs& p, int epi, int max_rows, int mblk, hipStream_t s);
+// Weight-streaming kernel (stream.hip) for segments of a few rows: bf16 x bf16, or
+// e4m3 x e4m3 (fp8 = true, W8A8 with p.a_scale / p.b_scale).
+bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8);
+int stream_out_cols(int N, int epi);   // widest output columns per streaming task (0: unsupported)
+hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s);
 int gemm_out_cols_per_tile(int tile, int epi);
 hipError_t launch_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,
                                     hipStream_t s);

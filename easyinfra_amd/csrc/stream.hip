@@ -23,6 +23,11 @@
 //     re-read from L2, not HBM).
 // MFMA v_mfma_f32_16x16x32_bf16 operand layout: lane l holds row/column l%16 and k
 // 8*(l/16)..+7 of a 32-wide k step; D lane l holds rows 4*(l/16)+r of column l%16.
+// FP8 (W8A8: e4m3 activations and weights, v_mfma_scale_f32_16x16x128_f8f6f4 with unit
+// block scales): one 128-wide k step per 128 bytes of a row, the same byte addresses per
+// lane as the bf16 64-wide step; lane l feeds bytes 16q..+15 and 64+16q..+15 (q = l/16) of
+// both operands, so the k sum is exact whatever order the instruction adds; the per-row
+// activation scale and per-output-channel weight scale are applied in the epilogue.
 #include "common.h"
 #include "kernels.h"
 
@@ -113,21 +118,38 @@ __device__ __forceinline__ void stream_load(StreamStage<NFRAG, MBLK>& st, __amdg
 #endif
 }
 
-template <int NFRAG, int MBLK>
+__device__ __forceinline__ i32x8_t cat_fp8(const bf16x8_t& lo, const bf16x8_t& hi) {
+  const u32x4_t a = __builtin_bit_cast(u32x4_t, lo);
+  const u32x4_t b = __builtin_bit_cast(u32x4_t, hi);
+  return i32x8_t{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+}
+
+template <int NFRAG, int MBLK, bool FP8>
 __device__ __forceinline__ void stream_mma(f32x4_t (&acc)[MBLK][NFRAG], const StreamStage<NFRAG, MBLK>& st) {
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
+  if constexpr (FP8) {
 #pragma unroll
     for (int m = 0; m < MBLK; ++m)
 #pragma unroll
       for (int f = 0; f < NFRAG; ++f)
-        acc[m][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.a[m][h], st.b[f][h], acc[m][f], 0, 0, 0);
+        acc[m][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(cat_fp8(st.a[m][0], st.a[m][1]),
+                                                                      cat_fp8(st.b[f][0], st.b[f][1]), acc[m][f],
+                                                                      0, 0, 0, 127, 0, 127);
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int m = 0; m < MBLK; ++m)
+#pragma unroll
+        for (int f = 0; f < NFRAG; ++f)
+          acc[m][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.a[m][h], st.b[f][h], acc[m][f], 0, 0, 0);
+  }
 }
 
 // EPI kEpiSiluBF16: fragments [0, NFRAG/2) are gate rows col0 + 16f + (0..15), fragments
 // [NFRAG/2, NFRAG) the matching up rows; else NFRAG fragments of 16 consecutive output
-// columns.  W waves split K (K/64 is a multiple of W*U: the launcher picks W and U).
-template <int EPI, int NFRAG, int MBLK, int U, int W>
+// columns.  W waves split K (the k-step count is a multiple of W*U: the launcher picks W
+// and U).  FP8: both operands e4m3 (W8A8), 128-wide k steps.
+template <int EPI, int NFRAG, int MBLK, int U, int W, bool FP8>
 __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p) {
   constexpr bool SILU = (EPI == kEpiSiluBF16);
   static_assert(!SILU || NFRAG % 2 == 0, "SiLU pairs gate and up fragments");
@@ -149,22 +171,24 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
 
   const int lr = lane & 15;
   const uint32_t kq = static_cast<uint32_t>((lane >> 4) * 16);   // this lane's 16-byte k chunk
+  constexpr int EB = FP8 ? 1 : 2;                                   // bytes per element
   const __amdgpu_buffer_rsrc_t ra =
-      make_rsrc(static_cast<const uint16_t*>(p.a) + k0, (p.a_rows_cap * p.lda - k0) * 2);
+      make_rsrc(static_cast<const uint8_t*>(p.a) + k0 * EB, (p.a_rows_cap * p.lda - k0) * EB);
   const __amdgpu_buffer_rsrc_t rb =
-      make_rsrc(static_cast<const uint16_t*>(p.b) + static_cast<long long>(expert) * p.b_estride + k0,
-                (p.b_estride - k0) * 2);
+      make_rsrc(static_cast<const uint8_t*>(p.b) + (static_cast<long long>(expert) * p.b_estride + k0) * EB,
+                (p.b_estride - k0) * EB);
   uint32_t a_voff[MBLK], b_voff[NFRAG];
 #pragma unroll
   for (int m = 0; m < MBLK; ++m) {
     const int r = min(row0 + m * 16 + lr, row_end - 1);
     const long long src = p.a_rows ? static_cast<long long>(p.a_rows[r]) : static_cast<long long>(r);
-    a_voff[m] = static_cast<uint32_t>(src * p.lda * 2) + kq;
+    a_voff[m] = static_cast<uint32_t>(src * p.lda * EB) + kq;
   }
+  int wrow[NFRAG];
 #pragma unroll
   for (int f = 0; f < NFRAG; ++f) {
-    const int wr = SILU ? (f < G ? col0 + f * 16 + lr : p.up_off + col0 + (f - G) * 16 + lr) : col0 + f * 16 + lr;
-    b_voff[f] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb * 2) + kq;
+    wrow[f] = SILU ? (f < G ? col0 + f * 16 + lr : p.up_off + col0 + (f - G) * 16 + lr) : col0 + f * 16 + lr;
+    b_voff[f] = static_cast<uint32_t>(static_cast<long long>(wrow[f]) * p.ldb * EB) + kq;
   }
 
   f32x4_t acc[MBLK][NFRAG];
@@ -177,7 +201,7 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   // U divides the step count (the launcher picks it), so the loop body has no branch and
   // the compiler's vmcnt waits stay exact; fetch indices are clamped to the last step, so
   // the final iterations re-read it (L2 hits) instead of branching.
-  const int KW = p.K / 64 / W;   // k steps of this wave
+  const int KW = p.K / (FP8 ? 128 : 64) / W;   // k steps (128 bytes of a row each) of this wave
   const int s0 = wave * KW;
   const int s_last = s0 + KW - 1;
   StreamStage<NFRAG, MBLK> st[U];
@@ -192,7 +216,7 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       stream_load<NFRAG, MBLK>(st[(u + U - 1) % U], ra, rb, a_voff, b_voff, min(s + u + U - 1, s_last));
-      stream_mma<NFRAG, MBLK>(acc, st[u]);
+      stream_mma<NFRAG, MBLK, FP8>(acc, st[u]);
 #if defined(__HIP_DEVICE_COMPILE__)
       __builtin_amdgcn_sched_barrier(0);   // keep the ring order: the scheduler would batch all loads
 #endif
@@ -226,8 +250,13 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
       if constexpr (SILU) {
 #pragma unroll
         for (int f = 0; f < G; ++f) {
-          const float g = acc[m][f][r] * rs;
-          const float u = acc[m][G + f][r] * rs;
+          float g = acc[m][f][r] * rs;
+          float u = acc[m][G + f][r] * rs;
+          if (p.b_scale) {
+            const float* sc = p.b_scale + static_cast<long long>(expert) * p.nb_rows;
+            g *= sc[wrow[f]];
+            u *= sc[wrow[G + f]];
+          }
           static_cast<uint16_t*>(p.c)[static_cast<long long>(row) * p.ldc + col0 + f * 16 + lr] =
               f32_to_bf16(silu_f32(g) * u);
         }
@@ -237,7 +266,8 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
           const int col = col0 + f * 16 + lr;
           const long long off =
               static_cast<long long>(split) * p.c_split_stride + static_cast<long long>(row) * p.ldc + col;
-          const float v = acc[m][f][r] * rs;
+          const float v =
+              acc[m][f][r] * rs * (p.b_scale ? p.b_scale[static_cast<long long>(expert) * p.nb_rows + wrow[f]] : 1.f);
           if constexpr (EPI == kEpiStoreF32) static_cast<float*>(p.c)[off] = v;
           else static_cast<uint16_t*>(p.c)[off] = f32_to_bf16(v);
         }
@@ -246,63 +276,86 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   }
 }
 
-template <int EPI, int NFRAG, int MBLK, int W>
+// Upper bound on tasks (the grid): row chunks per segment <= rows/BM + 1.
+long long stream_tasks_bound(const GemmArgs& p, int max_rows, int nfrag, int mblk, int epi) {
+  const int bm = 16 * mblk;
+  const int cols = (epi == kEpiSiluBF16 ? 8 : 16) * nfrag;
+  const long long chunks = (static_cast<long long>(max_rows) + bm - 1) / bm + p.S;
+  return chunks * (p.N / cols) * p.k_split;
+}
+
+template <int EPI, int NFRAG, int MBLK, int W, bool FP8>
 hipError_t launch_stream_w(const GemmArgs& p, dim3 g, hipStream_t s) {
   const dim3 b(64 * W);
-  if ((p.K / 64 / W) % 2 == 0) hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 2, W>), g, b, 0, s, p);
-  else hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 1, W>), g, b, 0, s, p);
+  if ((p.K / (FP8 ? 128 : 64) / W) % 2 == 0)
+    hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 2, W, FP8>), g, b, 0, s, p);
+  else
+    hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 1, W, FP8>), g, b, 0, s, p);
   return hipGetLastError();
 }
 
-template <int EPI, int NFRAG, int MBLK>
+template <int EPI, int NFRAG, int MBLK, bool FP8>
 hipError_t launch_stream_cfg(const GemmArgs& p, int max_rows, hipStream_t s) {
-  constexpr int BM = 16 * MBLK;
-  constexpr int COLS = (EPI == kEpiSiluBF16) ? 8 * NFRAG : 16 * NFRAG;
-  const long long chunks = (static_cast<long long>(max_rows) + BM - 1) / BM + p.S;   // bound
-  const long long tasks = chunks * (p.N / COLS) * p.k_split;
+  const long long tasks = stream_tasks_bound(p, max_rows, NFRAG, MBLK, EPI);
   if (tasks > 0x7fffffffll) return hipErrorInvalidValue;
   const dim3 g(static_cast<unsigned>(tasks > 0 ? tasks : 1));
-  if ((p.K / 64) % 4 == 0) return launch_stream_w<EPI, NFRAG, MBLK, 4>(p, g, s);
-  return launch_stream_w<EPI, NFRAG, MBLK, 1>(p, g, s);
+  // Split K over the workgroup's waves only while each wave keeps >= 16 steps: shorter
+  // streams spend a large share of their time filling and draining the register ring.
+  const int ks = p.K / (FP8 ? 128 : 64);
+  if (ks % 4 == 0 && ks / 4 >= 16) return launch_stream_w<EPI, NFRAG, MBLK, 4, FP8>(p, g, s);
+  if (ks % 2 == 0 && ks / 2 >= 16) return launch_stream_w<EPI, NFRAG, MBLK, 2, FP8>(p, g, s);
+  return launch_stream_w<EPI, NFRAG, MBLK, 1, FP8>(p, g, s);
 }
 
-template <int EPI, int NFRAG>
+template <int EPI, int NFRAG, bool FP8>
 hipError_t launch_stream_nf(const GemmArgs& p, int max_rows, int mblk, hipStream_t s) {
-  return mblk == 1 ? launch_stream_cfg<EPI, NFRAG, 1>(p, max_rows, s) : launch_stream_cfg<EPI, NFRAG, 2>(p, max_rows, s);
+  return mblk == 1 ? launch_stream_cfg<EPI, NFRAG, 1, FP8>(p, max_rows, s)
+                   : launch_stream_cfg<EPI, NFRAG, 2, FP8>(p, max_rows, s);
 }
 
-// Fragments per wave: 8 (measured best: each activation load feeds 8 weight fragments),
-// fewer when the output width does not divide.
-int stream_nfrag(const GemmArgs& p, int epi) {
+// Fragments per wave: as many as the output width allows, up to 8 (each activation load
+// then feeds 8 weight fragments: measured the fastest on large decode layers), but no more
+// than keeps about 4 workgroups per CU in the grid (small layers are latency-bound).
+int stream_nfrag(const GemmArgs& p, int epi, int max_rows, int mblk) {
   const int per = epi == kEpiSiluBF16 ? 8 : 16;   // output columns per fragment
-  for (int nf = 8; nf >= 2; nf /= 2)
-    if (p.N % (per * nf) == 0) return nf;
-  return 0;
+  int best = 0;
+  for (int nf = 2; nf <= 8; nf *= 2) {
+    if (p.N % (per * nf) != 0) continue;
+    if (best == 0 || stream_tasks_bound(p, max_rows, nf, mblk, epi) >= 4ll * kNumCu) best = nf;
+  }
+  return best;
 }
 
 }  // namespace
 
-bool stream_gemm_supported(const GemmArgs& p, int epi) { return p.K % 64 == 0 && stream_nfrag(p, epi) > 0; }
-
-int stream_out_cols(int N, int epi) {
-  GemmArgs p{};
-  p.N = N;
-  const int nf = stream_nfrag(p, epi);
-  return nf * (epi == kEpiSiluBF16 ? 8 : 16);
+bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8) {
+  return p.K % (fp8 ? 128 : 64) == 0 && stream_nfrag(p, epi, 0, 1) > 0;
 }
 
-hipError_t launch_stream_gemm(const GemmArgs& p, int epi, int max_rows, int mblk, hipStream_t s) {
-  const int nf = stream_nfrag(p, epi);
-  if (p.K % 64 != 0 || nf == 0) return hipErrorInvalidValue;
-#define EIMOE_STREAM_NF(E)                                                   \
+int stream_out_cols(int N, int epi) {
+  const int per = epi == kEpiSiluBF16 ? 8 : 16;
+  for (int nf = 8; nf >= 2; nf /= 2)
+    if (N % (per * nf) == 0) return per * nf;
+  return 0;
+}
+
+hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s) {
+  const int nf = stream_nfrag(p, epi, max_rows, mblk);
+  if (p.K % (fp8 ? 128 : 64) != 0 || nf == 0) return hipErrorInvalidValue;
+#define EIMOE_STREAM_NF(E, F8)                                               \
   switch (nf) {                                                              \
-    case 8: return launch_stream_nf<E, 8>(p, max_rows, mblk, s);             \
-    case 4: return launch_stream_nf<E, 4>(p, max_rows, mblk, s);             \
-    default: return launch_stream_nf<E, 2>(p, max_rows, mblk, s);            \
+    case 8: return launch_stream_nf<E, 8, F8>(p, max_rows, mblk, s);         \
+    case 4: return launch_stream_nf<E, 4, F8>(p, max_rows, mblk, s);         \
+    default: return launch_stream_nf<E, 2, F8>(p, max_rows, mblk, s);        \
   }
-  if (epi == kEpiSiluBF16) { EIMOE_STREAM_NF(kEpiSiluBF16) }
-  if (epi == kEpiStoreBF16) { EIMOE_STREAM_NF(kEpiStoreBF16) }
-  EIMOE_STREAM_NF(kEpiStoreF32)
+  if (fp8) {
+    if (epi == kEpiSiluBF16) { EIMOE_STREAM_NF(kEpiSiluBF16, true) }
+    if (epi == kEpiStoreBF16) { EIMOE_STREAM_NF(kEpiStoreBF16, true) }
+    EIMOE_STREAM_NF(kEpiStoreF32, true)
+  }
+  if (epi == kEpiSiluBF16) { EIMOE_STREAM_NF(kEpiSiluBF16, false) }
+  if (epi == kEpiStoreBF16) { EIMOE_STREAM_NF(kEpiStoreBF16, false) }
+  EIMOE_STREAM_NF(kEpiStoreF32, false)
 #undef EIMOE_STREAM_NF
 }
 

@@ -27,10 +27,12 @@ def _segments(counts):
     return off, torch.as_tensor(off)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4])
-def test_w8a8_gate_up_matches_oracle(dev, tile):
-    g = torch.Generator().manual_seed(tile)
-    H, I, T = 256, 256, 50
+# tile 5 = the weight-streaming kernel (fp8 operands on the 16x16x128 fp8 MFMA); H=1024
+# reaches its 4-wave K split with a 2-deep register ring, H=256 the unsplit ring.
+@pytest.mark.parametrize("tile,H", [(1, 256), (2, 256), (3, 256), (4, 256), (5, 256), (5, 1024)])
+def test_w8a8_gate_up_matches_oracle(dev, tile, H):
+    g = torch.Generator().manual_seed(tile + H)
+    I, T = 256, 50
     counts = [0, 37, 300, 5]
     E = len(counts)
     off, off_t = _segments(counts)
@@ -53,7 +55,7 @@ def test_w8a8_gate_up_matches_oracle(dev, tile):
         torch.testing.assert_close(h[a:b], ref, rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 2), (4, 1)])
+@pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 2), (4, 1), (5, 1), (5, 2)])
 def test_w8a8_down_matches_oracle(dev, tile, k_split):
     g = torch.Generator().manual_seed(10 + tile)
     H, I = 256, 512
