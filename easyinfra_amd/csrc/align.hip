@@ -16,6 +16,9 @@
 // 64 ids, no atomics).  A prefix over waves and experts turns it into per-(wave,
 // expert) write cursors.  Pass 2 re-reads the slice; each id's slot is its cursor
 // plus its rank among equal ids below it in the wave, so the result is stable.
+// Both passes fetch kAlignBatch rows of 64 ids per lane before using any of them: one
+// workgroup does all the work, so a dependent load per 64 ids would put a memory
+// latency on every step (tens of microseconds at 16-25k routed pairs).
 #include "common.h"
 #include "kernels.h"
 
@@ -23,6 +26,23 @@ namespace eimoe {
 
 constexpr int kAlignWaves = 16;
 constexpr int kAlignThreads = kAlignWaves * 64;
+constexpr int kAlignBatch = 8;
+
+// Local expert of flat ids i0 + 64r + lane (r < kAlignBatch), -1 outside [.., end) or the window.
+__device__ __forceinline__ void load_batch(const int32_t* __restrict__ ids, int i0, int end, int lane, int e_lo,
+                                           int n_loc, int (&e)[kAlignBatch]) {
+  int raw[kAlignBatch];
+#pragma unroll
+  for (int r = 0; r < kAlignBatch; ++r) {
+    const int i = i0 + r * 64 + lane;
+    raw[r] = i < end ? ids[i] : INT32_MIN;
+  }
+#pragma unroll
+  for (int r = 0; r < kAlignBatch; ++r) {
+    const int g = raw[r] == INT32_MIN ? -1 : raw[r] - e_lo;
+    e[r] = (g >= 0 && g < n_loc) ? g : -1;
+  }
+}
 
 __device__ __forceinline__ uint64_t match_mask(int e, int nbits, uint64_t valid) {
   uint64_t m = valid;
@@ -59,17 +79,17 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int32_t* __r
   __syncthreads();
 
   // pass 1: per-wave histogram
-  for (int i0 = beg; i0 < end; i0 += 64) {
-    const int i = i0 + lane;
-    int e = -1;
-    if (i < end) {
-      const int g = ids[i] - e_lo;
-      if (g >= 0 && g < n_loc) e = g;
+  for (int i0 = beg; i0 < end; i0 += 64 * kAlignBatch) {
+    int eb[kAlignBatch];
+    load_batch(ids, i0, end, lane, e_lo, n_loc, eb);
+#pragma unroll
+    for (int r = 0; r < kAlignBatch; ++r) {
+      const int e = eb[r];
+      const uint64_t valid = __ballot(e >= 0);
+      const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
+      if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1)
+        hist[w * n_loc + e] += __popcll(m);
     }
-    const uint64_t valid = __ballot(e >= 0);
-    const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
-    if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1)
-      hist[w * n_loc + e] += __popcll(m);
   }
   __syncthreads();
 
@@ -110,25 +130,26 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int32_t* __r
 
   // pass 2: stable placement.  All lanes read their cursor before the group leader
   // advances it; one wave's LDS operations execute in program order.
-  for (int i0 = beg; i0 < end; i0 += 64) {
-    const int i = i0 + lane;
-    int e = -1;
-    if (i < end) {
-      const int g = ids[i] - e_lo;
-      if (g >= 0 && g < n_loc) e = g;
-    }
-    const uint64_t valid = __ballot(e >= 0);
-    const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
-    int p = -1;
-    if (e >= 0) p = hist[w * n_loc + e] + __popcll(m & lt_mask);
-    __builtin_amdgcn_wave_barrier();
-    if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1)
-      hist[w * n_loc + e] += __popcll(m);
-    if (i < end) {
-      pos[i] = p;
-      if (p >= 0) {
-        sorted_flat[p] = i;
-        sorted_tok[p] = i / k;
+  for (int i0 = beg; i0 < end; i0 += 64 * kAlignBatch) {
+    int eb[kAlignBatch];
+    load_batch(ids, i0, end, lane, e_lo, n_loc, eb);
+#pragma unroll
+    for (int r = 0; r < kAlignBatch; ++r) {
+      const int i = i0 + r * 64 + lane;
+      const int e = eb[r];
+      const uint64_t valid = __ballot(e >= 0);
+      const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
+      int p = -1;
+      if (e >= 0) p = hist[w * n_loc + e] + __popcll(m & lt_mask);
+      __builtin_amdgcn_wave_barrier();
+      if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1)
+        hist[w * n_loc + e] += __popcll(m);
+      if (i < end) {
+        pos[i] = p;
+        if (p >= 0) {
+          sorted_flat[p] = i;
+          sorted_tok[p] = i / k;
+        }
       }
     }
   }

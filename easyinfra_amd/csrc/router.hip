@@ -113,14 +113,16 @@ static hipError_t launch_router_lv(const float* logits, int T, int E, int k, int
   return hipGetLastError();
 }
 
+// Lane groups of 16 up to 128 experts: each selection round is a 4-step butterfly shared
+// by 4 tokens of the wave (a 64-lane group would spend 6 steps on one token).
 hipError_t launch_router_topk(const float* logits, int T, int E, int k, int renorm, int32_t* ids, float* w,
                               hipStream_t s) {
   if (E <= 8) return launch_router_lv<8, 1>(logits, T, E, k, renorm, ids, w, s);
   if (E <= 16) return launch_router_lv<16, 1>(logits, T, E, k, renorm, ids, w, s);
-  if (E <= 32) return launch_router_lv<32, 1>(logits, T, E, k, renorm, ids, w, s);
-  if (E <= 64) return launch_router_lv<64, 1>(logits, T, E, k, renorm, ids, w, s);
-  if (E <= 128) return launch_router_lv<64, 2>(logits, T, E, k, renorm, ids, w, s);
-  if (E <= 256) return launch_router_lv<64, 4>(logits, T, E, k, renorm, ids, w, s);
+  if (E <= 32) return launch_router_lv<16, 2>(logits, T, E, k, renorm, ids, w, s);
+  if (E <= 64) return launch_router_lv<16, 4>(logits, T, E, k, renorm, ids, w, s);
+  if (E <= 128) return launch_router_lv<16, 8>(logits, T, E, k, renorm, ids, w, s);
+  if (E <= 256) return launch_router_lv<32, 8>(logits, T, E, k, renorm, ids, w, s);
   return launch_router_lv<64, 8>(logits, T, E, k, renorm, ids, w, s);
 }
 
