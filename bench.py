@@ -47,9 +47,13 @@ def parse():
     ap.add_argument("--no-suite", action="store_true",
                     help="skip the other workloads (tiny fp32 layer, DeepSeek-V2-Lite, Qwen3-30B-A3B local share, "
                          "fp8 Mixtral)")
+    ap.add_argument("--profile-case", default=None, metavar="NAME:T[:uniform][:w8a8]",
+                    help="profiling driver: 12 cache-flushed fused-layer calls of one workload (names as in "
+                         "easyinfra_amd.workloads.SHAPES); prints no JSON line")
     ap.add_argument("--traffic-run", action="store_true",
                     help="counter-collection driver: a 1 GiB device copy (known bytes, calibrates FETCH_SIZE/"
-                         "WRITE_SIZE) followed by two fused prefill layers; prints no JSON line")
+                         "WRITE_SIZE) followed by two fused prefill layers and two 64-token decode layers; prints "
+                         "no JSON line")
     return ap.parse_args()
 
 
@@ -157,6 +161,9 @@ def traffic_run(torch, ops, shape, make_inputs, tokens):
     inp = make_inputs(shape, tokens, device="cuda")
     for _ in range(2):
         ops.fused_moe(inp.x, inp.logits, shape.top_k, inp.w_gate_up, inp.w_down, renormalize=shape.renormalize)
+    dx, dl = inp.x[:64].contiguous(), inp.logits[:64].contiguous()
+    for _ in range(2):   # the 64-token decode batch (weight-streaming kernels)
+        ops.fused_moe(dx, dl, shape.top_k, inp.w_gate_up, inp.w_down, renormalize=shape.renormalize)
     torch.cuda.synchronize()
     print("traffic run done", flush=True)
 
@@ -249,6 +256,27 @@ def suite(torch, ops, mix_inp, steps, warmup):
     return out
 
 
+def profile_case(torch, ops, spec):
+    from easyinfra_amd.workloads import SHAPES, make_inputs
+    parts = spec.split(":")
+    shape, T = SHAPES[parts[0]], int(parts[1])
+    inp = make_inputs(shape, T, device="cuda", uniform_twin="uniform" in parts[2:])
+    wgu, wd, scales = inp.w_gate_up.to(torch.bfloat16), inp.w_down.to(torch.bfloat16), None
+    w8a8 = "w8a8" in parts[2:]
+    if w8a8:
+        qgu, sgu = ops.quantize_weights_fp8(wgu)
+        qd, sd = ops.quantize_weights_fp8(wd)
+        wgu, wd, scales = qgu, qd, (sgu, sd)
+    flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+    for _ in range(12):
+        flush.sum()
+        ops.fused_moe(inp.x, inp.logits, shape.top_k, wgu, wd, renormalize=shape.renormalize,
+                      shared_gate_up=inp.shared_gate_up, shared_down=inp.shared_down,
+                      expert_range=inp.expert_range, w_scales=scales, w8a8=w8a8)
+    torch.cuda.synchronize()
+    print("profile case done:", spec, flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -264,6 +292,9 @@ def main():
     shape = MIXTRAL_8X7B
     if args.traffic_run:
         traffic_run(torch, ops, shape, make_inputs, args.tokens)
+        return
+    if args.profile_case:
+        profile_case(torch, ops, args.profile_case)
         return
     T = args.tokens
     inp = make_inputs(shape, T, device=dev)
