@@ -670,8 +670,12 @@ int gemm_out_cols_per_tile(int tile, int epi) {
 int gemm_pick_tile(int epi, int max_rows, int S, int N) {
   const double avg = static_cast<double>(max_rows) / (S > 0 ? S : 1);
   int t;
-  if (avg >= 256) t = kTileL;
-  else if (avg >= 96) t = kTileM;
+  if (avg >= 256) {
+    // fewer 256x256 tiles than CUs (a dense shared-expert launch, say) leaves CUs idle: step down
+    const long long mt = static_cast<long long>(max_rows) / 256 + S;
+    t = (N % gemm_out_cols_per_tile(kTileL, epi) == 0 && mt * (N / gemm_out_cols_per_tile(kTileL, epi)) < kNumCu)
+            ? kTileM : kTileL;
+  } else if (avg >= 96) t = kTileM;
   else if (avg >= 24) t = kTileS;
   else t = kTileXS;
   while (t != kTileXS && N % gemm_out_cols_per_tile(t, epi) != 0) ++t;

@@ -7,12 +7,53 @@
 // Weights: exp(l - max) / sum over the k picks (renormalise) or over all experts.
 //
 // Layout: a wave holds 64/LPT tokens; lane group of LPT lanes owns one token row,
-// each lane VPL logits (experts li, li+LPT, ...).  Argmax rounds are butterfly
-// reductions inside the lane group.
+// each lane VPL logits (experts li, li+LPT, ...).  Argmax rounds are all-reduces inside
+// the lane group (DPP lane permutes up to 16 lanes).
 #include "common.h"
 #include "kernels.h"
 
 namespace eimoe {
+
+// All-reduce inside a lane group of LPT lanes.  Groups of up to 16 lanes stay inside one
+// DPP row, so the steps are VALU lane permutes (quad xor-1, quad xor-2, half-row mirror, row
+// mirror) instead of LDS-routed shuffles; wider groups finish with shuffles.  Both reductions
+// (max by value then lowest index; sum) combine every lane of the group whatever the pairing.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+__device__ __forceinline__ void take_better(float& bv, int& bi, float ov, int oi) {
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+template <int LPT>
+__device__ __forceinline__ void group_argmax(float& bv, int& bi) {
+  if constexpr (LPT >= 2) take_better(bv, bi, dpp_f<0xB1>(bv), dpp_i<0xB1>(bi));     // quad_perm [1,0,3,2]
+  if constexpr (LPT >= 4) take_better(bv, bi, dpp_f<0x4E>(bv), dpp_i<0x4E>(bi));     // quad_perm [2,3,0,1]
+  if constexpr (LPT >= 8) take_better(bv, bi, dpp_f<0x141>(bv), dpp_i<0x141>(bi));   // row_half_mirror
+  if constexpr (LPT >= 16) take_better(bv, bi, dpp_f<0x140>(bv), dpp_i<0x140>(bi));  // row_mirror
+#pragma unroll
+  for (int m = 16; m < LPT; m <<= 1) take_better(bv, bi, __shfl_xor(bv, m, LPT), __shfl_xor(bi, m, LPT));
+}
+
+template <int LPT>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (LPT >= 2) x += dpp_f<0xB1>(x);
+  if constexpr (LPT >= 4) x += dpp_f<0x4E>(x);
+  if constexpr (LPT >= 8) x += dpp_f<0x141>(x);
+  if constexpr (LPT >= 16) x += dpp_f<0x140>(x);
+#pragma unroll
+  for (int m = 16; m < LPT; m <<= 1) x += __shfl_xor(x, m, LPT);
+  return x;
+}
 
 template <int LPT, int VPL, int KMAX>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
@@ -55,15 +96,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
             }
           }
         }
-#pragma unroll
-        for (int m = LPT / 2; m >= 1; m >>= 1) {
-          const float ov = __shfl_xor(bv, m, LPT);
-          const int oi = __shfl_xor(bi, m, LPT);
-          if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-          }
-        }
+        group_argmax<LPT>(bv, bi);
         selv[r] = bv;
         seli[r] = bi;
         if (bi != 0x7fffffff && (bi % LPT) == li) avail &= ~(1u << (bi / LPT));
@@ -82,9 +115,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
         const int e = li + j * LPT;
         if (tv && e < E) part += expf(v[j] - mx);
       }
-#pragma unroll
-      for (int m = LPT / 2; m >= 1; m >>= 1) part += __shfl_xor(part, m, LPT);
-      denom = part;
+      denom = group_sum<LPT>(part);
     }
     if (tv) {
 #pragma unroll

@@ -316,10 +316,11 @@ hipError_t launch_stream_nf(const GemmArgs& p, int max_rows, int mblk, hipStream
 // Fragments per wave: as many as the output width allows, up to 8 (each activation load
 // then feeds 8 weight fragments: measured the fastest on large decode layers), but no more
 // than keeps about 4 workgroups per CU in the grid (small layers are latency-bound).
-int stream_nfrag(const GemmArgs& p, int epi, int max_rows, int mblk) {
+int stream_nfrag(const GemmArgs& p, int epi, int max_rows, int mblk, bool fp8) {
   const int per = epi == kEpiSiluBF16 ? 8 : 16;   // output columns per fragment
+  const int cap = fp8 ? 4 : 8;                    // e4m3: half the steps per task; 4 measured ~7 % faster
   int best = 0;
-  for (int nf = 2; nf <= 8; nf *= 2) {
+  for (int nf = 2; nf <= cap; nf *= 2) {
     if (p.N % (per * nf) != 0) continue;
     if (best == 0 || stream_tasks_bound(p, max_rows, nf, mblk, epi) >= 4ll * kNumCu) best = nf;
   }
@@ -329,7 +330,7 @@ int stream_nfrag(const GemmArgs& p, int epi, int max_rows, int mblk) {
 }  // namespace
 
 bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8) {
-  return p.K % (fp8 ? 128 : 64) == 0 && stream_nfrag(p, epi, 0, 1) > 0;
+  return p.K % (fp8 ? 128 : 64) == 0 && stream_nfrag(p, epi, 0, 1, fp8) > 0;
 }
 
 int stream_out_cols(int N, int epi) {
@@ -340,7 +341,7 @@ int stream_out_cols(int N, int epi) {
 }
 
 hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s) {
-  const int nf = stream_nfrag(p, epi, max_rows, mblk);
+  const int nf = stream_nfrag(p, epi, max_rows, mblk, fp8);
   if (p.K % (fp8 ? 128 : 64) != 0 || nf == 0) return hipErrorInvalidValue;
 #define EIMOE_STREAM_NF(E, F8)                                               \
   switch (nf) {                                                              \
