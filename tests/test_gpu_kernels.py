@@ -231,7 +231,10 @@ def test_gemm_rejects_bad_shapes(dev):
 
 # --------------------------------------------------------------------------- fp8
 @pytest.mark.parametrize("shape,dtype", [((7, 1000), torch.float32), ((64, 4096), torch.bfloat16),
-                                         ((3, 5), torch.float32), ((2, 16, 96), torch.bfloat16)])
+                                         ((3, 5), torch.float32), ((2, 16, 96), torch.bfloat16),
+                                         ((128, 14336), torch.bfloat16), ((5, 8192), torch.float32),
+                                         ((9, 2052), torch.float32), ((3, 20000), torch.bfloat16),
+                                         ((4, 100), torch.bfloat16)])
 def test_quantize_rows_fp8_bit_exact(dev, shape, dtype):
     g = torch.Generator().manual_seed(shape[0])
     x = (torch.randn(*shape, generator=g) * 0.3).to(dtype)
