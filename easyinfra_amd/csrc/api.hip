@@ -64,18 +64,22 @@ int check_tile(int tile, int epi, int N) {
 // Each candidate split is charged its padded rounds, in units of one full-K tile, plus the
 // HBM round trip of its extra partial planes (written here, read back by the combine);
 // small launches also split until they fill the GPU twice over.
-int pick_down_split(int max_rows, int n_local, int H, int I, int y_elem) {
+int pick_down_split(int max_rows, int n_local, int H, int I, int y_elem, bool w8a8) {
   const int tile = gemm_pick_tile(kEpiStoreF32, max_rows, n_local, H);
   if (tile == kTileXS) {
-    // Few rows per segment: the weight-streaming kernel (bf16 weights) runs one 4-wave
-    // workgroup per (segment, column group, 32-row chunk, split).  Split until there are
-    // about 6 workgroups per CU, keeping K/64 per split a multiple of 8 (4 waves x 2 steps).
-    const int cols = std::max(stream_out_cols(H, kEpiStoreF32), 16);
+    // Few rows per segment: the weight-streaming kernel runs one workgroup per (segment,
+    // column group, 32-row chunk, split).  Split until there are about 6 workgroups per CU
+    // while the split divides the K steps (64 bf16 / 128 e4m3 bytes each) and leaves each
+    // split >= 8 of them (Mixtral 64-token down, bf16: split 1/2/4/8 = 200/192/181/190 us).
+    const int steps = w8a8 ? I / 128 : I / 64;
+    const int cols = std::max(stream_out_cols(H, kEpiStoreF32, w8a8), 16);
     const long long tasks = (std::min<long long>(n_local, max_rows) + (max_rows + 31) / 32) * (H / cols);
     int split = 1;
-    while (split < 8 && tasks * split < 6ll * kNumCu && I % (64 * 8 * split * 2) == 0) split *= 2;
+    while (split < 8 && tasks * split < 6ll * kNumCu && steps % (split * 2) == 0 && steps / (split * 2) >= 8)
+      split *= 2;
     return split;
   }
+  if (w8a8) I /= 2;   // e4m3 tiles run at twice the bf16 rate: cost them as half the K
   const int bm = tile == kTileL ? 256 : tile == kTileM ? 128 : tile == kTileS ? 32 : 16;
   const int bn = gemm_out_cols_per_tile(tile, kEpiStoreF32);
   const long long mt = std::min<long long>(n_local, max_rows) + max_rows / bm;   // bound on m-tiles
@@ -110,9 +114,8 @@ FusedLayout fused_layout(int T, int H, int I, int k, int n_local, int Is, int ou
   FusedLayout L{};
   const size_t A = static_cast<size_t>(T) * k;
   L.y_dtype = ((flags & EIMOE_Y_F32) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
-  // W8A8 planes cover K slices that are multiples of 128: pick the split on I/2 in 64s.
-  L.k_split = pick_down_split(static_cast<int>(A), n_local, H, (flags & EIMOE_W8A8) ? I / 2 : I,
-                              static_cast<int>(elem_size(L.y_dtype)));
+  L.k_split = pick_down_split(static_cast<int>(A), n_local, H, I, static_cast<int>(elem_size(L.y_dtype)),
+                              (flags & EIMOE_W8A8) != 0);
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -250,6 +253,32 @@ int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, in
   return hip_check(launch_align(topk_ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos,
                                 S(stream)),
                    "align");
+}
+
+int eimoe_route_align(const float* logits, int T, int E, int k, int renormalize, int e_lo, int n_local,
+                      int32_t* topk_ids, float* topk_weights, int32_t* counts, int32_t* offsets,
+                      int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream) {
+  if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
+  if (E < 1 || E > EIMOE_MAX_EXPERTS) return fail(EIMOE_ERR_SHAPE, "E=%d outside [1,%d]", E, EIMOE_MAX_EXPERTS);
+  if (k < 1 || k > E || k > EIMOE_MAX_TOPK)
+    return fail(EIMOE_ERR_SHAPE, "k=%d outside [1,min(E=%d,%d)]", k, E, EIMOE_MAX_TOPK);
+  if (n_local < 1 || n_local > EIMOE_MAX_EXPERTS)
+    return fail(EIMOE_ERR_SHAPE, "n_local=%d outside [1,%d]", n_local, EIMOE_MAX_EXPERTS);
+  if (e_lo < 0) return fail(EIMOE_ERR_SHAPE, "e_lo=%d < 0", e_lo);
+  if (static_cast<long long>(T) * k > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "T*k overflows int32");
+  REQUIRE_PTR(counts);
+  REQUIRE_PTR(offsets);
+  if (T > 0) {
+    REQUIRE_PTR(logits);
+    REQUIRE_PTR(topk_ids);
+    REQUIRE_PTR(topk_weights);
+    REQUIRE_PTR(sorted_flat);
+    REQUIRE_PTR(sorted_tok);
+    REQUIRE_PTR(pos);
+  }
+  return hip_check(launch_route_align(logits, T, E, k, renormalize ? 1 : 0, e_lo, n_local, topk_ids, topk_weights,
+                                      counts, offsets, sorted_flat, sorted_tok, pos, S(stream)),
+                   "route_align");
 }
 
 int eimoe_counts_to_offsets(const int32_t* counts, int n_seg, int32_t* offsets, void* stream) {
@@ -517,11 +546,9 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   const hipStream_t s = S(stream);
   const int A = T * k;
   int rc;
-  if ((rc = hip_check(launch_router_topk(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, ids, w, s),
-                      "router_topk")))
-    return rc;
-  if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos, s),
-                      "align")))
+  if ((rc = hip_check(launch_route_align(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, e_lo, n_local, ids, w,
+                                         counts, offsets, sorted_flat, sorted_tok, pos, s),
+                      "route_align")))
     return rc;
   if (flags & EIMOE_W8A8) {
     // activations quantised per token (x) and per row (h); both GEMMs on the fp8 MFMA

@@ -44,6 +44,12 @@ hipError_t launch_router_topk(const float* logits, int T, int E, int k, int reno
 size_t align_lds_bytes(int n_loc);
 hipError_t launch_align(const int32_t* ids, int T, int k, int e_lo, int n_loc, int32_t* counts, int32_t* offsets,
                         int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, hipStream_t s);
+// Router then align; one workgroup runs both when route_align_fused() (small batches),
+// otherwise the two kernels above.
+bool route_align_fused(int T, int E, int k, int n_loc);
+hipError_t launch_route_align(const float* logits, int T, int E, int k, int renorm, int e_lo, int n_loc,
+                              int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
+                              int32_t* sorted_tok, int32_t* pos, hipStream_t s);
 hipError_t launch_counts_to_offsets(const int32_t* counts, int S, int32_t* offsets, hipStream_t s);
 hipError_t launch_gather_rows(const void* x, int row_bytes, const int32_t* rows, const int32_t* num_rows,
                               int max_rows, void* xs, hipStream_t s);
@@ -58,7 +64,7 @@ int gemm_pick_tile(int epi, int max_rows, int S, int N);
 // Weight-streaming kernel (stream.hip) for segments of a few rows: bf16 x bf16, or
 // e4m3 x e4m3 (fp8 = true, W8A8 with p.a_scale / p.b_scale).
 bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8);
-int stream_out_cols(int N, int epi);   // widest output columns per streaming task (0: unsupported)
+int stream_out_cols(int N, int epi, bool fp8);   // widest output columns per streaming task (0: unsupported)
 hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s);
 int gemm_out_cols_per_tile(int tile, int epi);
 hipError_t launch_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,

@@ -9,124 +9,17 @@
 // Layout: a wave holds 64/LPT tokens; lane group of LPT lanes owns one token row,
 // each lane VPL logits (experts li, li+LPT, ...).  Argmax rounds are all-reduces inside
 // the lane group (DPP lane permutes up to 16 lanes).
-#include "common.h"
 #include "kernels.h"
+#include "routing.h"
 
 namespace eimoe {
-
-// All-reduce inside a lane group of LPT lanes.  Groups of up to 16 lanes stay inside one
-// DPP row, so the steps are VALU lane permutes (quad xor-1, quad xor-2, half-row mirror, row
-// mirror) instead of LDS-routed shuffles; wider groups finish with shuffles.  Both reductions
-// (max by value then lowest index; sum) combine every lane of the group whatever the pairing.
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
-}
-
-__device__ __forceinline__ void take_better(float& bv, int& bi, float ov, int oi) {
-  if (ov > bv || (ov == bv && oi < bi)) {
-    bv = ov;
-    bi = oi;
-  }
-}
-
-template <int LPT>
-__device__ __forceinline__ void group_argmax(float& bv, int& bi) {
-  if constexpr (LPT >= 2) take_better(bv, bi, dpp_f<0xB1>(bv), dpp_i<0xB1>(bi));     // quad_perm [1,0,3,2]
-  if constexpr (LPT >= 4) take_better(bv, bi, dpp_f<0x4E>(bv), dpp_i<0x4E>(bi));     // quad_perm [2,3,0,1]
-  if constexpr (LPT >= 8) take_better(bv, bi, dpp_f<0x141>(bv), dpp_i<0x141>(bi));   // row_half_mirror
-  if constexpr (LPT >= 16) take_better(bv, bi, dpp_f<0x140>(bv), dpp_i<0x140>(bi));  // row_mirror
-#pragma unroll
-  for (int m = 16; m < LPT; m <<= 1) take_better(bv, bi, __shfl_xor(bv, m, LPT), __shfl_xor(bi, m, LPT));
-}
-
-template <int LPT>
-__device__ __forceinline__ float group_sum(float x) {
-  if constexpr (LPT >= 2) x += dpp_f<0xB1>(x);
-  if constexpr (LPT >= 4) x += dpp_f<0x4E>(x);
-  if constexpr (LPT >= 8) x += dpp_f<0x141>(x);
-  if constexpr (LPT >= 16) x += dpp_f<0x140>(x);
-#pragma unroll
-  for (int m = 16; m < LPT; m <<= 1) x += __shfl_xor(x, m, LPT);
-  return x;
-}
 
 template <int LPT, int VPL, int KMAX>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
                                                           int renorm, int32_t* __restrict__ ids,
                                                           float* __restrict__ wts) {
-  constexpr int TPW = 64 / LPT;
-  const int lane = threadIdx.x & 63;
-  const int sub = lane / LPT;
-  const int li = lane % LPT;
-  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int nwaves = (gridDim.x * blockDim.x) >> 6;
-  const float NEG_INF = -__builtin_inff();
-
-  for (int t0 = wave * TPW; t0 < T; t0 += nwaves * TPW) {
-    const int t = t0 + sub;
-    const bool tv = t < T;
-    float v[VPL];
-    uint32_t avail = 0;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const int e = li + j * LPT;
-      const bool ok = tv && e < E;
-      v[j] = ok ? logits[static_cast<long long>(t) * E + e] : NEG_INF;
-      if (ok) avail |= 1u << j;
-    }
-    float selv[KMAX];
-    int seli[KMAX];
-#pragma unroll
-    for (int r = 0; r < KMAX; ++r) {
-      if (r < k) {
-        float bv = NEG_INF;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-          const int e = li + j * LPT;
-          if ((avail >> j) & 1u) {
-            if (v[j] > bv || (v[j] == bv && e < bi)) {
-              bv = v[j];
-              bi = e;
-            }
-          }
-        }
-        group_argmax<LPT>(bv, bi);
-        selv[r] = bv;
-        seli[r] = bi;
-        if (bi != 0x7fffffff && (bi % LPT) == li) avail &= ~(1u << (bi / LPT));
-      }
-    }
-    const float mx = selv[0];
-    float denom = 0.f;
-    if (renorm) {
-#pragma unroll
-      for (int r = 0; r < KMAX; ++r)
-        if (r < k) denom += expf(selv[r] - mx);
-    } else {
-      float part = 0.f;
-#pragma unroll
-      for (int j = 0; j < VPL; ++j) {
-        const int e = li + j * LPT;
-        if (tv && e < E) part += expf(v[j] - mx);
-      }
-      denom = group_sum<LPT>(part);
-    }
-    if (tv) {
-#pragma unroll
-      for (int r = 0; r < KMAX; ++r) {
-        if (r < k && (r % LPT) == li) {
-          ids[static_cast<long long>(t) * k + r] = seli[r];
-          wts[static_cast<long long>(t) * k + r] = expf(selv[r] - mx) / denom;
-        }
-      }
-    }
-  }
+  route_rows<LPT, VPL, KMAX, false>(logits, T, E, k, renorm, ids, wts, nullptr,
+                                    (blockIdx.x * blockDim.x + threadIdx.x) >> 6, (gridDim.x * blockDim.x) >> 6);
 }
 
 template <int LPT, int VPL>
@@ -155,6 +48,74 @@ hipError_t launch_router_topk(const float* logits, int T, int E, int k, int reno
   if (E <= 128) return launch_router_lv<16, 8>(logits, T, E, k, renorm, ids, w, s);
   if (E <= 256) return launch_router_lv<32, 8>(logits, T, E, k, renorm, ids, w, s);
   return launch_router_lv<64, 8>(logits, T, E, k, renorm, ids, w, s);
+}
+
+// Router and align in one workgroup, for batches its 16 waves route in a few steps: the
+// ids stay in LDS between the two phases, and one launch (a few microseconds of dispatch
+// and cold-cache latency at decode sizes) replaces two.  Same outputs as the two kernels.
+template <int LPT, int VPL, int KMAX>
+__global__ __launch_bounds__(kAlignThreads) void route_align_kernel(
+    const float* __restrict__ logits, int T, int E, int k, int renorm, int e_lo, int n_loc, int32_t* __restrict__ ids,
+    float* __restrict__ wts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_flat, int32_t* __restrict__ sorted_tok, int32_t* __restrict__ pos) {
+  extern __shared__ int lds[];
+  int* s_ids = lds + align_lds_ints(n_loc);   // [T*k] after the align's histogram
+  route_rows<LPT, VPL, KMAX, true>(logits, T, E, k, renorm, ids, wts, s_ids, threadIdx.x >> 6, kAlignWaves);
+  __syncthreads();
+  align_rows(s_ids, T * k, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, lds);
+}
+
+namespace {
+
+constexpr int kRouteAlignMaxSteps = 2;          // routing steps of the 16 waves
+constexpr size_t kRouteAlignMaxLds = 64 * 1024;
+
+int router_lanes(int E) { return E <= 8 ? 8 : E <= 128 ? 16 : 32; }
+
+size_t route_align_lds_bytes(int T, int k, int n_loc) {
+  return (static_cast<size_t>(align_lds_ints(n_loc)) + static_cast<size_t>(T) * k) * sizeof(int);
+}
+
+template <int LPT, int VPL>
+hipError_t launch_route_align_lv(const float* logits, int T, int E, int k, int renorm, int e_lo, int n_loc,
+                                 int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
+                                 int32_t* sorted_tok, int32_t* pos, hipStream_t s) {
+  const size_t lds = route_align_lds_bytes(T, k, n_loc);
+  if (k <= 8)
+    hipLaunchKernelGGL((route_align_kernel<LPT, VPL, 8>), dim3(1), dim3(kAlignThreads), lds, s, logits, T, E, k,
+                       renorm, e_lo, n_loc, ids, w, counts, offsets, sorted_flat, sorted_tok, pos);
+  else
+    hipLaunchKernelGGL((route_align_kernel<LPT, VPL, 32>), dim3(1), dim3(kAlignThreads), lds, s, logits, T, E, k,
+                       renorm, e_lo, n_loc, ids, w, counts, offsets, sorted_flat, sorted_tok, pos);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool route_align_fused(int T, int E, int k, int n_loc) {
+  const long long per_step = static_cast<long long>(kAlignWaves) * (64 / router_lanes(E));
+  return T >= 1 && E <= 256 && (T + per_step - 1) / per_step <= kRouteAlignMaxSteps &&
+         route_align_lds_bytes(T, k, n_loc) <= kRouteAlignMaxLds;
+}
+
+hipError_t launch_route_align(const float* logits, int T, int E, int k, int renorm, int e_lo, int n_loc,
+                              int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
+                              int32_t* sorted_tok, int32_t* pos, hipStream_t s) {
+  if (!route_align_fused(T, E, k, n_loc)) {
+    hipError_t e = launch_router_topk(logits, T, E, k, renorm, ids, w, s);
+    if (e != hipSuccess) return e;
+    return launch_align(ids, T, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, s);
+  }
+#define EIMOE_RA(L, V) \
+  return launch_route_align_lv<L, V>(logits, T, E, k, renorm, e_lo, n_loc, ids, w, counts, offsets, sorted_flat, \
+                                     sorted_tok, pos, s)
+  if (E <= 8) EIMOE_RA(8, 1);
+  if (E <= 16) EIMOE_RA(16, 1);
+  if (E <= 32) EIMOE_RA(16, 2);
+  if (E <= 64) EIMOE_RA(16, 4);
+  if (E <= 128) EIMOE_RA(16, 8);
+  EIMOE_RA(32, 8);   // E <= 256 here (wider rows hold k <= 32 picks in too many registers)
+#undef EIMOE_RA
 }
 
 }  // namespace eimoe

@@ -1,0 +1,258 @@
+// Device bodies of the router (softmax -> top-k) and of the align (stable counting sort
+// by expert), shared by their own kernels and by the single-workgroup kernel that runs
+// both for small batches.  Reference citations are at the kernels (router.hip, align.hip).
+#pragma once
+#include "common.h"
+
+namespace eimoe {
+
+// All-reduce inside a lane group of LPT lanes.  Groups of up to 16 lanes stay inside one
+// DPP row, so the steps are VALU lane permutes (quad xor-1, quad xor-2, half-row mirror, row
+// mirror) instead of LDS-routed shuffles; wider groups finish with shuffles.  Both reductions
+// (max by value then lowest index; sum) combine every lane of the group whatever the pairing.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+__device__ __forceinline__ void take_better(float& bv, int& bi, float ov, int oi) {
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+template <int LPT>
+__device__ __forceinline__ void group_argmax(float& bv, int& bi) {
+  if constexpr (LPT >= 2) take_better(bv, bi, dpp_f<0xB1>(bv), dpp_i<0xB1>(bi));     // quad_perm [1,0,3,2]
+  if constexpr (LPT >= 4) take_better(bv, bi, dpp_f<0x4E>(bv), dpp_i<0x4E>(bi));     // quad_perm [2,3,0,1]
+  if constexpr (LPT >= 8) take_better(bv, bi, dpp_f<0x141>(bv), dpp_i<0x141>(bi));   // row_half_mirror
+  if constexpr (LPT >= 16) take_better(bv, bi, dpp_f<0x140>(bv), dpp_i<0x140>(bi));  // row_mirror
+#pragma unroll
+  for (int m = 16; m < LPT; m <<= 1) take_better(bv, bi, __shfl_xor(bv, m, LPT), __shfl_xor(bi, m, LPT));
+}
+
+template <int LPT>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (LPT >= 2) x += dpp_f<0xB1>(x);
+  if constexpr (LPT >= 4) x += dpp_f<0x4E>(x);
+  if constexpr (LPT >= 8) x += dpp_f<0x141>(x);
+  if constexpr (LPT >= 16) x += dpp_f<0x140>(x);
+#pragma unroll
+  for (int m = 16; m < LPT; m <<= 1) x += __shfl_xor(x, m, LPT);
+  return x;
+}
+
+// Route tokens wave, wave + nwaves, ... (TPW tokens per wave and step): softmax, top-k
+// by logit (ties to the lower id), weights over the picks or over all experts.  With
+// TO_LDS the ids are also stored to lds_ids[t*k + r] for an align in the same workgroup.
+template <int LPT, int VPL, int KMAX, bool TO_LDS>
+__device__ __forceinline__ void route_rows(const float* __restrict__ logits, int T, int E, int k, int renorm,
+                                           int32_t* __restrict__ ids, float* __restrict__ wts, int* lds_ids,
+                                           int wave, int nwaves) {
+  constexpr int TPW = 64 / LPT;
+  const int lane = threadIdx.x & 63;
+  const int sub = lane / LPT;
+  const int li = lane % LPT;
+  const float NEG_INF = -__builtin_inff();
+
+  for (int t0 = wave * TPW; t0 < T; t0 += nwaves * TPW) {
+    const int t = t0 + sub;
+    const bool tv = t < T;
+    float v[VPL];
+    uint32_t avail = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int e = li + j * LPT;
+      const bool ok = tv && e < E;
+      v[j] = ok ? logits[static_cast<long long>(t) * E + e] : NEG_INF;
+      if (ok) avail |= 1u << j;
+    }
+    float selv[KMAX];
+    int seli[KMAX];
+#pragma unroll
+    for (int r = 0; r < KMAX; ++r) {
+      if (r < k) {
+        float bv = NEG_INF;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+          const int e = li + j * LPT;
+          if ((avail >> j) & 1u) {
+            if (v[j] > bv || (v[j] == bv && e < bi)) {
+              bv = v[j];
+              bi = e;
+            }
+          }
+        }
+        group_argmax<LPT>(bv, bi);
+        selv[r] = bv;
+        seli[r] = bi;
+        if (bi != 0x7fffffff && (bi % LPT) == li) avail &= ~(1u << (bi / LPT));
+      }
+    }
+    const float mx = selv[0];
+    float denom = 0.f;
+    if (renorm) {
+#pragma unroll
+      for (int r = 0; r < KMAX; ++r)
+        if (r < k) denom += expf(selv[r] - mx);
+    } else {
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        const int e = li + j * LPT;
+        if (tv && e < E) part += expf(v[j] - mx);
+      }
+      denom = group_sum<LPT>(part);
+    }
+    if (tv) {
+#pragma unroll
+      for (int r = 0; r < KMAX; ++r) {
+        if (r < k && (r % LPT) == li) {
+          ids[static_cast<long long>(t) * k + r] = seli[r];
+          if constexpr (TO_LDS) lds_ids[t * k + r] = seli[r];
+          wts[static_cast<long long>(t) * k + r] = expf(selv[r] - mx) / denom;
+        }
+      }
+    }
+  }
+}
+
+constexpr int kAlignWaves = 16;
+constexpr int kAlignThreads = kAlignWaves * 64;
+constexpr int kAlignBatch = 8;
+
+// Local expert of flat ids i0 + 64r + lane (r < kAlignBatch), -1 outside [.., end) or the window.
+__device__ __forceinline__ void load_batch(const int32_t* __restrict__ ids, int i0, int end, int lane, int e_lo,
+                                           int n_loc, int (&e)[kAlignBatch]) {
+  int raw[kAlignBatch];
+#pragma unroll
+  for (int r = 0; r < kAlignBatch; ++r) {
+    const int i = i0 + r * 64 + lane;
+    raw[r] = i < end ? ids[i] : INT32_MIN;
+  }
+#pragma unroll
+  for (int r = 0; r < kAlignBatch; ++r) {
+    const int g = raw[r] == INT32_MIN ? -1 : raw[r] - e_lo;
+    e[r] = (g >= 0 && g < n_loc) ? g : -1;
+  }
+}
+
+__device__ __forceinline__ uint64_t match_mask(int e, int nbits, uint64_t valid) {
+  uint64_t m = valid;
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t bal = __ballot(bit);
+    m &= bit ? bal : ~bal;
+  }
+  return m;
+}
+
+constexpr int align_lds_ints(int n_loc) { return kAlignWaves * n_loc + 2 * n_loc + 1; }
+
+// Counting sort of N = T*k flat ids by local expert, in one workgroup of kAlignThreads
+// threads; lds holds align_lds_ints(n_loc) ints.  ids may point to global memory or LDS.
+__device__ __forceinline__ void align_rows(const int32_t* __restrict__ ids, int N, int k, int e_lo, int n_loc,
+                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                           int32_t* __restrict__ sorted_flat, int32_t* __restrict__ sorted_tok,
+                                           int32_t* __restrict__ pos, int* lds) {
+  int* hist = lds;                              // [kAlignWaves][n_loc]
+  int* tot = lds + kAlignWaves * n_loc;         // [n_loc]
+  int* offs = tot + n_loc;                      // [n_loc + 1]
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+
+  int chunk = (N + kAlignWaves - 1) / kAlignWaves;
+  chunk = (chunk + 63) & ~63;
+  const int beg = w * chunk;
+  const int end = min(N, beg + chunk);
+  const int nbits = n_loc > 1 ? 32 - __clz(n_loc - 1) : 0;
+
+  for (int i = tid; i < kAlignWaves * n_loc; i += kAlignThreads) hist[i] = 0;
+  __syncthreads();
+
+  // pass 1: per-wave histogram
+  for (int i0 = beg; i0 < end; i0 += 64 * kAlignBatch) {
+    int eb[kAlignBatch];
+    load_batch(ids, i0, end, lane, e_lo, n_loc, eb);
+#pragma unroll
+    for (int r = 0; r < kAlignBatch; ++r) {
+      const int e = eb[r];
+      const uint64_t valid = __ballot(e >= 0);
+      const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
+      if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1)
+        hist[w * n_loc + e] += __popcll(m);
+    }
+  }
+  __syncthreads();
+
+  // per expert: exclusive prefix over waves and total count
+  for (int e = tid; e < n_loc; e += kAlignThreads) {
+    int run = 0;
+    for (int ww = 0; ww < kAlignWaves; ++ww) {
+      const int c = hist[ww * n_loc + e];
+      hist[ww * n_loc + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+    counts[e] = run;
+  }
+  __syncthreads();
+
+  // exclusive scan over experts (wave 0)
+  if (w == 0) {
+    const int per = (n_loc + 63) / 64;
+    const int b0 = lane * per;
+    int s = 0;
+    for (int j = 0; j < per; ++j)
+      if (b0 + j < n_loc) s += tot[b0 + j];
+    const int incl = wave_incl_scan(s);
+    int run = incl - s;
+    for (int j = 0; j < per; ++j) {
+      if (b0 + j < n_loc) {
+        offs[b0 + j] = run;
+        run += tot[b0 + j];
+      }
+    }
+    if (lane == 63) offs[n_loc] = incl;
+  }
+  __syncthreads();
+  for (int i = tid; i <= n_loc; i += kAlignThreads) offsets[i] = offs[i];
+  for (int i = tid; i < kAlignWaves * n_loc; i += kAlignThreads) hist[i] += offs[i % n_loc];
+  __syncthreads();
+
+  // pass 2: stable placement.  All lanes read their cursor before the group leader
+  // advances it; one wave's LDS operations execute in program order.
+  for (int i0 = beg; i0 < end; i0 += 64 * kAlignBatch) {
+    int eb[kAlignBatch];
+    load_batch(ids, i0, end, lane, e_lo, n_loc, eb);
+#pragma unroll
+    for (int r = 0; r < kAlignBatch; ++r) {
+      const int i = i0 + r * 64 + lane;
+      const int e = eb[r];
+      const uint64_t valid = __ballot(e >= 0);
+      const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
+      int p = -1;
+      if (e >= 0) p = hist[w * n_loc + e] + __popcll(m & lt_mask);
+      __builtin_amdgcn_wave_barrier();
+      if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1)
+        hist[w * n_loc + e] += __popcll(m);
+      if (i < end) {
+        pos[i] = p;
+        if (p >= 0) {
+          sorted_flat[p] = i;
+          sorted_tok[p] = i / k;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace eimoe

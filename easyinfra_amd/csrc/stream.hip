@@ -28,6 +28,8 @@
 // lane as the bf16 64-wide step; lane l feeds bytes 16q..+15 and 64+16q..+15 (q = l/16) of
 // both operands, so the k sum is exact whatever order the instruction adds; the per-row
 // activation scale and per-output-channel weight scale are applied in the epilogue.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -145,10 +147,13 @@ __device__ __forceinline__ void stream_mma(f32x4_t (&acc)[MBLK][NFRAG], const St
   }
 }
 
+constexpr int kShortSteps = 4;   // k steps per wave held in flight whole by the short-stream mode
+
 // EPI kEpiSiluBF16: fragments [0, NFRAG/2) are gate rows col0 + 16f + (0..15), fragments
 // [NFRAG/2, NFRAG) the matching up rows; else NFRAG fragments of 16 consecutive output
 // columns.  W waves split K (the k-step count is a multiple of W*U: the launcher picks W
-// and U).  FP8: both operands e4m3 (W8A8), 128-wide k steps.
+// and U; U = 0 is the short-stream mode, at most kShortSteps steps per wave).  FP8: both
+// operands e4m3 (W8A8), 128-wide k steps.
 template <int EPI, int NFRAG, int MBLK, int U, int W, bool FP8>
 __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p) {
   constexpr bool SILU = (EPI == kEpiSiluBF16);
@@ -204,22 +209,34 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   const int KW = p.K / (FP8 ? 128 : 64) / W;   // k steps (128 bytes of a row each) of this wave
   const int s0 = wave * KW;
   const int s_last = s0 + KW - 1;
-  StreamStage<NFRAG, MBLK> st[U];
+  if constexpr (U == 0) {
+    // Short stream (KW <= kShortSteps, small grids): every load of the wave is issued
+    // before the first MFMA, so the wave waits for one memory round trip, not KW.
+    StreamStage<NFRAG, MBLK> st[kShortSteps];
 #pragma unroll
-  for (int u = 0; u < U - 1; ++u) {
-    stream_load<NFRAG, MBLK>(st[u], ra, rb, a_voff, b_voff, min(s0 + u, s_last));
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_sched_barrier(0);   // stage order must match the loop's for exact vmcnt waits
-#endif
-  }
-  for (int s = s0; s <= s_last; s += U) {
+    for (int u = 0; u < kShortSteps; ++u)
+      if (u < KW) stream_load<NFRAG, MBLK>(st[u], ra, rb, a_voff, b_voff, s0 + u);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      stream_load<NFRAG, MBLK>(st[(u + U - 1) % U], ra, rb, a_voff, b_voff, min(s + u + U - 1, s_last));
-      stream_mma<NFRAG, MBLK, FP8>(acc, st[u]);
+    for (int u = 0; u < kShortSteps; ++u)
+      if (u < KW) stream_mma<NFRAG, MBLK, FP8>(acc, st[u]);
+  } else {
+    StreamStage<NFRAG, MBLK> st[U];
+#pragma unroll
+    for (int u = 0; u < U - 1; ++u) {
+      stream_load<NFRAG, MBLK>(st[u], ra, rb, a_voff, b_voff, min(s0 + u, s_last));
 #if defined(__HIP_DEVICE_COMPILE__)
-      __builtin_amdgcn_sched_barrier(0);   // keep the ring order: the scheduler would batch all loads
+      __builtin_amdgcn_sched_barrier(0);   // stage order must match the loop's for exact vmcnt waits
 #endif
+    }
+    for (int s = s0; s <= s_last; s += U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        stream_load<NFRAG, MBLK>(st[(u + U - 1) % U], ra, rb, a_voff, b_voff, min(s + u + U - 1, s_last));
+        stream_mma<NFRAG, MBLK, FP8>(acc, st[u]);
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_sched_barrier(0);   // keep the ring order: the scheduler would batch all loads
+#endif
+      }
     }
   }
   if constexpr (W > 1) {
@@ -276,12 +293,20 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   }
 }
 
-// Upper bound on tasks (the grid): row chunks per segment <= rows/BM + 1.
+// Upper bound on tasks (the grid): a segment of n > 0 rows has ceil(n/BM) <= floor(n/BM) + 1
+// row chunks, the rows sum to at most max_rows and at most min(S, max_rows) segments are
+// non-empty.
 long long stream_tasks_bound(const GemmArgs& p, int max_rows, int nfrag, int mblk, int epi) {
   const int bm = 16 * mblk;
   const int cols = (epi == kEpiSiluBF16 ? 8 : 16) * nfrag;
-  const long long chunks = (static_cast<long long>(max_rows) + bm - 1) / bm + p.S;
+  const long long chunks = static_cast<long long>(max_rows) / bm + std::min(p.S, max_rows);
   return chunks * (p.N / cols) * p.k_split;
+}
+
+template <int EPI, int NFRAG, int MBLK, int W, bool FP8>
+hipError_t launch_stream_short(const GemmArgs& p, dim3 g, hipStream_t s) {
+  hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 0, W, FP8>), g, dim3(64 * W), 0, s, p);
+  return hipGetLastError();
 }
 
 template <int EPI, int NFRAG, int MBLK, int W, bool FP8>
@@ -302,8 +327,18 @@ hipError_t launch_stream_cfg(const GemmArgs& p, int max_rows, hipStream_t s) {
   // Split K over the workgroup's waves only while each wave keeps >= 16 steps: shorter
   // streams spend a large share of their time filling and draining the register ring.
   const int ks = p.K / (FP8 ? 128 : 64);
-  if (ks % 4 == 0 && ks / 4 >= 16) return launch_stream_w<EPI, NFRAG, MBLK, 4, FP8>(p, g, s);
-  if (ks % 2 == 0 && ks / 2 >= 16) return launch_stream_w<EPI, NFRAG, MBLK, 2, FP8>(p, g, s);
+  const int w = (ks % 4 == 0 && ks / 4 >= 16) ? 4 : (ks % 2 == 0 && ks / 2 >= 16) ? 2 : 1;
+  if constexpr (NFRAG == 2) {
+    // Grids of fewer than ~8 waves per CU (a few tokens) are latency-bound: each wave's
+    // stream is a chain of memory round trips.  Split K over 4 or 8 waves so each holds
+    // at most kShortSteps steps, all in flight at once.
+    if (tasks * w < 8ll * kNumCu) {
+      if (ks % 4 == 0 && ks / 4 <= kShortSteps) return launch_stream_short<EPI, NFRAG, MBLK, 4, FP8>(p, g, s);
+      if (ks % 8 == 0 && ks / 8 <= kShortSteps) return launch_stream_short<EPI, NFRAG, MBLK, 8, FP8>(p, g, s);
+    }
+  }
+  if (w == 4) return launch_stream_w<EPI, NFRAG, MBLK, 4, FP8>(p, g, s);
+  if (w == 2) return launch_stream_w<EPI, NFRAG, MBLK, 2, FP8>(p, g, s);
   return launch_stream_w<EPI, NFRAG, MBLK, 1, FP8>(p, g, s);
 }
 
@@ -333,9 +368,9 @@ bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8) {
   return p.K % (fp8 ? 128 : 64) == 0 && stream_nfrag(p, epi, 0, 1, fp8) > 0;
 }
 
-int stream_out_cols(int N, int epi) {
+int stream_out_cols(int N, int epi, bool fp8) {
   const int per = epi == kEpiSiluBF16 ? 8 : 16;
-  for (int nf = 8; nf >= 2; nf /= 2)
+  for (int nf = fp8 ? 4 : 8; nf >= 2; nf /= 2)
     if (N % (per * nf) == 0) return per * nf;
   return 0;
 }

@@ -73,6 +73,28 @@ def align(topk_ids: torch.Tensor, n_local: int, e_lo: int = 0) -> dict:
     return out
 
 
+def route_align(logits: torch.Tensor, top_k: int, n_local: int, e_lo: int = 0,
+                renormalize: bool = True) -> Tuple[torch.Tensor, torch.Tensor, dict]:
+    """router_topk then align in one call (one launch for small batches) -> (ids, weights, align dict)."""
+    _req(logits, "logits", torch.float32, 2)
+    T, E = logits.shape
+    dev = logits.device
+    A = T * top_k
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    w = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    out = {
+        "counts": torch.empty(n_local, dtype=torch.int32, device=dev),
+        "offsets": torch.empty(n_local + 1, dtype=torch.int32, device=dev),
+        "sorted_flat": torch.empty(A, dtype=torch.int32, device=dev),
+        "sorted_tok": torch.empty(A, dtype=torch.int32, device=dev),
+        "pos": torch.empty(A, dtype=torch.int32, device=dev),
+    }
+    call("eimoe_route_align", logits.data_ptr(), T, E, top_k, int(renormalize), e_lo, n_local, ids.data_ptr(),
+         w.data_ptr(), out["counts"].data_ptr(), out["offsets"].data_ptr(), out["sorted_flat"].data_ptr(),
+         out["sorted_tok"].data_ptr(), out["pos"].data_ptr(), _stream(logits))
+    return ids, w, out
+
+
 def counts_to_offsets(counts: torch.Tensor) -> torch.Tensor:
     _req(counts, "counts", torch.int32, 1)
     off = torch.empty(counts.numel() + 1, dtype=torch.int32, device=counts.device)

@@ -80,6 +80,15 @@ int eimoe_router_topk(const float* logits, int T, int E, int k, int renormalize,
 int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, int32_t* counts, int32_t* offsets,
                 int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream);
 
+/* Router then align in one call: the outputs of eimoe_router_topk followed by eimoe_align on
+ * its ids, same arguments, same results bit for bit.  Small batches run both phases in one
+ * workgroup (one launch; the ids stay on chip between them).  Replaces the same reference code
+ * as the two calls: models/qwen3_moe/modeling_qwen3_moe.py:255-266, then
+ * generation/blocks/moe/base.py:343-364 and blocks/moe/moe_all2all.py:346-348. */
+int eimoe_route_align(const float* logits, int T, int E, int k, int renormalize, int e_lo, int n_local,
+                      int32_t* topk_ids, float* topk_weights, int32_t* counts, int32_t* offsets,
+                      int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream);
+
 /* Segment offsets from per-segment row counts (exclusive prefix sum, offsets[n_seg] = total).
  * Replaces the block schedule of TritonExperts.forward_ep (fused_moe.py:413-439) for callers that
  * pass pre-grouped rows (FusedMoE.forward_ep(hidden_states, expert_count), fused_moe.py:106-156). */

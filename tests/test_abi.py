@@ -56,6 +56,15 @@ def test_align_validation():
     assert _rc("eimoe_align", None, 4, 2, 0, 8, None, None, None, None, None, None) == _lib.ERR_NULL
 
 
+def test_route_align_validation():
+    n = [None] * 7
+    assert _rc("eimoe_route_align", None, 4, 8, 2, 1, 0, 0, *n, None) == _lib.ERR_SHAPE      # n_local 0
+    assert _rc("eimoe_route_align", None, 4, 8, 9, 1, 0, 8, *n, None) == _lib.ERR_SHAPE      # k > E
+    assert _rc("eimoe_route_align", None, 4, 8, 2, 1, -1, 8, *n, None) == _lib.ERR_SHAPE     # e_lo < 0
+    assert _rc("eimoe_route_align", None, 4, 0, 1, 1, 0, 8, *n, None) == _lib.ERR_SHAPE      # E 0
+    assert _rc("eimoe_route_align", None, 4, 8, 2, 1, 0, 8, *n, None) == _lib.ERR_NULL
+
+
 def test_gemm_validation():
     # H not a multiple of 64
     assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 100, 1, _lib.BF16, None, 100, 64, 1, 1, 1, 4, 1, 0,

@@ -29,7 +29,7 @@ def _segments(counts):
 
 # tile 5 = the weight-streaming kernel (fp8 operands on the 16x16x128 fp8 MFMA); H=1024
 # reaches its 4-wave K split with a 2-deep register ring, H=256 the unsplit ring.
-@pytest.mark.parametrize("tile,H", [(1, 256), (2, 256), (3, 256), (4, 256), (5, 256), (5, 1024)])
+@pytest.mark.parametrize("tile,H", [(1, 256), (2, 256), (3, 256), (4, 256), (5, 256), (5, 1024), (5, 4096)])
 def test_w8a8_gate_up_matches_oracle(dev, tile, H):
     g = torch.Generator().manual_seed(tile + H)
     I, T = 256, 50

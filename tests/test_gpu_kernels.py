@@ -97,6 +97,35 @@ def test_align_out_of_window_ids_dropped(dev):
     assert cpu(got["pos"]).tolist() == [-1, -1, 1, 0, -1, -1]
 
 
+# --------------------------------------------------------------------------- route + align
+# Batches small enough for the one-workgroup kernel (up to 2 routing steps of 16 waves:
+# 256 tokens at E <= 8, 128 at E <= 128, 64 at E <= 256) and ones just past it (two kernels).
+@pytest.mark.parametrize("T,E,k,e_lo,n_loc,renorm", [
+    (1, 8, 2, 0, 8, True), (64, 8, 2, 0, 8, True), (256, 8, 2, 0, 8, True), (257, 8, 2, 0, 8, True),
+    (32, 128, 8, 0, 32, True), (128, 128, 8, 32, 32, True), (129, 128, 8, 0, 32, True), (60, 64, 6, 0, 64, False),
+    (7, 256, 16, 50, 100, True), (64, 200, 20, 0, 200, False), (3, 300, 4, 0, 300, True), (5, 16, 1, 3, 1, True),
+])
+def test_route_align_bit_exact(dev, T, E, k, e_lo, n_loc, renorm):
+    g = torch.Generator().manual_seed(T * 31 + E)
+    logits = torch.randn(T, E, generator=g) * 2.0
+    logits[0, :4] = 1.5                                    # ties go to the lower id
+    ids, w, got = ops.route_align(logits.to(dev), k, n_loc, e_lo, renorm)
+    rid, rw = oracle.route_topk(logits, k, renorm)
+    assert torch.equal(cpu(ids), rid)
+    torch.testing.assert_close(cpu(w), rw, rtol=3e-6, atol=1e-7)
+    ref = oracle.align(rid.numpy(), n_loc, e_lo)
+    A = int(ref["offsets"][-1])
+    for key in ("counts", "offsets", "pos"):
+        assert np.array_equal(cpu(got[key]).numpy(), ref[key]), key
+    assert np.array_equal(cpu(got["sorted_flat"])[:A].numpy(), ref["sorted_flat"])
+    assert np.array_equal(cpu(got["sorted_tok"])[:A].numpy(), ref["sorted_tok"])
+
+
+def test_route_align_empty(dev):
+    ids, w, got = ops.route_align(torch.empty(0, 8, device=dev), 2, 8)
+    assert ids.shape == (0, 2) and cpu(got["offsets"]).tolist() == [0] * 9
+
+
 # --------------------------------------------------------------------------- gather / combine
 def test_gather_rows(dev):
     g = torch.Generator().manual_seed(5)
@@ -178,11 +207,13 @@ def test_down_gemm(dev, tile, k_split):
 
 
 # The weight-streaming kernel (tile 5) picks its column width (8/4/2 fragments), its K split
-# over 4 waves (when K/64 is a multiple of 4) and its register ring depth (2 or 1) from the
-# shapes; these cases reach every combination, rows past 32 per segment (several row chunks),
-# empty and one-row segments.  Nd is the down projection's output width (0: not run).
+# over waves and its register ring depth (2 or 1) from the shapes, or, for grids this small,
+# the short-stream mode (K split over 4 or 8 waves, at most 4 k-steps each, all in flight:
+# K = 256, 512, 768, 1024, 1536, 2048 here); these cases reach every combination, rows past
+# 32 per segment (several row chunks), empty and one-row segments.  Nd is the down
+# projection's output width (0: not run).
 @pytest.mark.parametrize("H,I,Nd", [(256, 256, 256), (192, 32, 0), (512, 96, 0), (64, 32, 0), (1408, 128, 1408),
-                                    (128, 320, 64), (256, 512, 192)])
+                                    (128, 320, 64), (256, 512, 192), (2048, 768, 2048), (1024, 1536, 256)])
 def test_stream_gemms_shapes(dev, H, I, Nd):
     g = torch.Generator().manual_seed(H + I + Nd)
     counts = [1, 0, 40, 7, 70]
