@@ -31,7 +31,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int32_t* __r
                                                               int32_t* __restrict__ sorted_tok,
                                                               int32_t* __restrict__ pos) {
   extern __shared__ int lds[];
-  align_rows(ids, N, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, lds);
+  align_rows<false>(ids, N, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, lds);
 }
 
 size_t align_lds_bytes(int n_loc) { return static_cast<size_t>(align_lds_ints(n_loc)) * sizeof(int); }

@@ -55,6 +55,7 @@ __device__ __forceinline__ void route_rows(const float* __restrict__ logits, int
                                            int32_t* __restrict__ ids, float* __restrict__ wts, int* lds_ids,
                                            int wave, int nwaves) {
   constexpr int TPW = 64 / LPT;
+  constexpr int KPL = (KMAX + LPT - 1) / LPT;   // picks held per lane
   const int lane = threadIdx.x & 63;
   const int sub = lane / LPT;
   const int li = lane % LPT;
@@ -72,51 +73,67 @@ __device__ __forceinline__ void route_rows(const float* __restrict__ logits, int
       v[j] = ok ? logits[static_cast<long long>(t) * E + e] : NEG_INF;
       if (ok) avail |= 1u << j;
     }
-    float selv[KMAX];
-    int seli[KMAX];
+    // Pick r lives in lane r % LPT of the group (slot r / LPT), so the rounds form a rolled
+    // loop: the kernel stays a few hundred instructions, which matters when it runs from a
+    // cold instruction cache (a decode step's router is a few microseconds of latency).
+    float myv[KPL];
+    int myi[KPL];
 #pragma unroll
-    for (int r = 0; r < KMAX; ++r) {
-      if (r < k) {
-        float bv = NEG_INF;
-        int bi = 0x7fffffff;
+    for (int j = 0; j < KPL; ++j) {
+      myv[j] = NEG_INF;
+      myi[j] = -1;
+    }
+    float mx = NEG_INF;
+#pragma unroll 1
+    for (int r = 0; r < k; ++r) {
+      float bv = NEG_INF;
+      int bi = 0x7fffffff;
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-          const int e = li + j * LPT;
-          if ((avail >> j) & 1u) {
-            if (v[j] > bv || (v[j] == bv && e < bi)) {
-              bv = v[j];
-              bi = e;
-            }
+      for (int j = 0; j < VPL; ++j) {
+        const int e = li + j * LPT;
+        if ((avail >> j) & 1u) {
+          if (v[j] > bv || (v[j] == bv && e < bi)) {
+            bv = v[j];
+            bi = e;
           }
         }
-        group_argmax<LPT>(bv, bi);
-        selv[r] = bv;
-        seli[r] = bi;
-        if (bi != 0x7fffffff && (bi % LPT) == li) avail &= ~(1u << (bi / LPT));
       }
-    }
-    const float mx = selv[0];
-    float denom = 0.f;
-    if (renorm) {
+      group_argmax<LPT>(bv, bi);
+      if (r == 0) mx = bv;
+      if (r % LPT == li) {
 #pragma unroll
-      for (int r = 0; r < KMAX; ++r)
-        if (r < k) denom += expf(selv[r] - mx);
-    } else {
-      float part = 0.f;
+        for (int j = 0; j < KPL; ++j)
+          if (j == r / LPT) {
+            myv[j] = bv;
+            myi[j] = bi;
+          }
+      }
+      if (bi != 0x7fffffff && (bi % LPT) == li) avail &= ~(1u << (bi / LPT));
+    }
+    float ex[KPL];
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      ex[j] = j * LPT + li < k ? expf(myv[j] - mx) : 0.f;
+      part += ex[j];
+    }
+    if (!renorm) {
+      part = 0.f;
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
         const int e = li + j * LPT;
         if (tv && e < E) part += expf(v[j] - mx);
       }
-      denom = group_sum<LPT>(part);
     }
+    const float denom = group_sum<LPT>(part);
     if (tv) {
 #pragma unroll
-      for (int r = 0; r < KMAX; ++r) {
-        if (r < k && (r % LPT) == li) {
-          ids[static_cast<long long>(t) * k + r] = seli[r];
-          if constexpr (TO_LDS) lds_ids[t * k + r] = seli[r];
-          wts[static_cast<long long>(t) * k + r] = expf(selv[r] - mx) / denom;
+      for (int j = 0; j < KPL; ++j) {
+        const int r = j * LPT + li;
+        if (r < k) {
+          ids[static_cast<long long>(t) * k + r] = myi[j];
+          if constexpr (TO_LDS) lds_ids[t * k + r] = myi[j];
+          wts[static_cast<long long>(t) * k + r] = ex[j] / denom;
         }
       }
     }
@@ -143,6 +160,15 @@ __device__ __forceinline__ void load_batch(const int32_t* __restrict__ ids, int 
   }
 }
 
+// e[r] for a wave-uniform r without indexing a register array (a select chain; the id
+// loops stay rolled, so the kernel's code stays small).
+__device__ __forceinline__ int pick(const int (&e)[kAlignBatch], int r) {
+  int v = e[0];
+#pragma unroll
+  for (int j = 1; j < kAlignBatch; ++j) v = r == j ? e[j] : v;
+  return v;
+}
+
 __device__ __forceinline__ uint64_t match_mask(int e, int nbits, uint64_t valid) {
   uint64_t m = valid;
   for (int b = 0; b < nbits; ++b) {
@@ -157,6 +183,11 @@ constexpr int align_lds_ints(int n_loc) { return kAlignWaves * n_loc + 2 * n_loc
 
 // Counting sort of N = T*k flat ids by local expert, in one workgroup of kAlignThreads
 // threads; lds holds align_lds_ints(n_loc) ints.  ids may point to global memory or LDS.
+// Each wave takes its ids in batches of kAlignBatch rows of 64; ROLLED walks a batch's
+// rows in a loop (small code: measured faster for a few hundred ids, where the kernel is
+// latency-bound), otherwise the rows are unrolled so their ballot chains overlap (faster
+// from a few thousand ids: 24 vs 36 us at 16384).
+template <bool ROLLED>
 __device__ __forceinline__ void align_rows(const int32_t* __restrict__ ids, int N, int k, int e_lo, int n_loc,
                                            int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
                                            int32_t* __restrict__ sorted_flat, int32_t* __restrict__ sorted_tok,
@@ -179,16 +210,20 @@ __device__ __forceinline__ void align_rows(const int32_t* __restrict__ ids, int 
   __syncthreads();
 
   // pass 1: per-wave histogram
+  auto count_row = [&](int e) {
+    const uint64_t valid = __ballot(e >= 0);
+    const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
+    if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1) hist[w * n_loc + e] += __popcll(m);
+  };
   for (int i0 = beg; i0 < end; i0 += 64 * kAlignBatch) {
     int eb[kAlignBatch];
     load_batch(ids, i0, end, lane, e_lo, n_loc, eb);
+    if constexpr (ROLLED) {
+#pragma unroll 1
+      for (int r = 0; r < kAlignBatch && i0 + r * 64 < end; ++r) count_row(pick(eb, r));
+    } else {
 #pragma unroll
-    for (int r = 0; r < kAlignBatch; ++r) {
-      const int e = eb[r];
-      const uint64_t valid = __ballot(e >= 0);
-      const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
-      if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1)
-        hist[w * n_loc + e] += __popcll(m);
+      for (int r = 0; r < kAlignBatch; ++r) count_row(eb[r]);
     }
   }
   __syncthreads();
@@ -230,27 +265,30 @@ __device__ __forceinline__ void align_rows(const int32_t* __restrict__ ids, int 
 
   // pass 2: stable placement.  All lanes read their cursor before the group leader
   // advances it; one wave's LDS operations execute in program order.
+  auto place_row = [&](int i, int e) {
+    const uint64_t valid = __ballot(e >= 0);
+    const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
+    int p = -1;
+    if (e >= 0) p = hist[w * n_loc + e] + __popcll(m & lt_mask);
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1) hist[w * n_loc + e] += __popcll(m);
+    if (i < end) {
+      pos[i] = p;
+      if (p >= 0) {
+        sorted_flat[p] = i;
+        sorted_tok[p] = i / k;
+      }
+    }
+  };
   for (int i0 = beg; i0 < end; i0 += 64 * kAlignBatch) {
     int eb[kAlignBatch];
     load_batch(ids, i0, end, lane, e_lo, n_loc, eb);
+    if constexpr (ROLLED) {
+#pragma unroll 1
+      for (int r = 0; r < kAlignBatch && i0 + r * 64 < end; ++r) place_row(i0 + r * 64 + lane, pick(eb, r));
+    } else {
 #pragma unroll
-    for (int r = 0; r < kAlignBatch; ++r) {
-      const int i = i0 + r * 64 + lane;
-      const int e = eb[r];
-      const uint64_t valid = __ballot(e >= 0);
-      const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
-      int p = -1;
-      if (e >= 0) p = hist[w * n_loc + e] + __popcll(m & lt_mask);
-      __builtin_amdgcn_wave_barrier();
-      if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1)
-        hist[w * n_loc + e] += __popcll(m);
-      if (i < end) {
-        pos[i] = p;
-        if (p >= 0) {
-          sorted_flat[p] = i;
-          sorted_tok[p] = i / k;
-        }
-      }
+      for (int r = 0; r < kAlignBatch; ++r) place_row(i0 + r * 64 + lane, eb[r]);
     }
   }
 }
