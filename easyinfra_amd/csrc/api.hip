@@ -64,8 +64,16 @@ int check_tile(int tile, int epi, int N) {
 // Each candidate split is charged its padded rounds, in units of one full-K tile, plus the
 // HBM round trip of its extra partial planes (written here, read back by the combine);
 // small launches also split until they fill the GPU twice over.
-int pick_down_split(int max_rows, int n_local, int H, int I, int y_elem, bool w8a8) {
-  const int tile = gemm_pick_tile(kEpiStoreF32, max_rows, n_local, H);
+int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int y_elem, bool w8a8) {
+  GemmArgs q{};
+  q.max_rows = max_rows;
+  q.rows_hint = rows_hint;
+  q.S = n_local;
+  q.N = H;
+  q.K = I;
+  q.k_split = 1;
+  q.nb_rows = H;
+  const int tile = gemm_pick_tile(q, kEpiStoreF32, w8a8);
   if (tile == kTileXS) {
     // Few rows per segment: the weight-streaming kernel runs one workgroup per (segment,
     // column group, 32-row chunk, split).  Split until there are about 6 workgroups per CU
@@ -79,10 +87,18 @@ int pick_down_split(int max_rows, int n_local, int H, int I, int y_elem, bool w8
       split *= 2;
     return split;
   }
+  // Experts too large for the caches, few rows each (decode batches on the LDS tiles): the
+  // launch streams weights at the HBM rate whatever the tile count, and split 2 measured
+  // best (Mixtral 64 tokens, 128x128 bf16: split 1/2/4/8 = 226/159/163/171 us; 32x128
+  // e4m3: 109/84/99/94).
+  const double expert_bytes = static_cast<double>(H) * I * (w8a8 ? 1 : 2);
+  if (expert_bytes >= 32.0 * 1024 * 1024 && tile != kTileL)
+    return (I / (w8a8 ? 128 : 64)) % 2 == 0 ? 2 : 1;
   if (w8a8) I /= 2;   // e4m3 tiles run at twice the bf16 rate: cost them as half the K
   const int bm = tile == kTileL ? 256 : tile == kTileM ? 128 : tile == kTileS ? 32 : 16;
   const int bn = gemm_out_cols_per_tile(tile, kEpiStoreF32);
-  const long long mt = std::min<long long>(n_local, max_rows) + max_rows / bm;   // bound on m-tiles
+  const int rows = rows_hint > 0 ? std::min(rows_hint, max_rows) : max_rows;
+  const long long mt = std::min<long long>(n_local, rows) + rows / bm;   // m-tiles (bound, or expected)
   const long long tiles = mt * (H / bn);
   constexpr double kTileFlops = 4.7e12;   // measured bf16 GEMM rate per CU, FLOP/s
   constexpr double kHbm = 5.0e12;         // achieved HBM rate for plane traffic, B/s
@@ -108,14 +124,23 @@ struct FusedLayout {
   size_t ids, w, counts, offsets, sorted_flat, sorted_tok, pos, h, y, sh_off, sh_h, sh_y, xq, sx, hq, sh, total;
   int k_split;
   int y_dtype;
+  int rows_hint;
 };
 
-FusedLayout fused_layout(int T, int H, int I, int k, int n_local, int Is, int out_dtype, int flags) {
+// Expected rows kept by an expert-parallel share of n_local of E experts (uniform routing):
+// the tile choice's estimate; the launches stay bounded by all T*k rows.
+int local_rows_hint(int T, int k, int E, int n_local) {
+  const long long A = static_cast<long long>(T) * k;
+  return n_local < E ? static_cast<int>(std::max<long long>(A * n_local / E, 1)) : static_cast<int>(A);
+}
+
+FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is, int out_dtype, int flags) {
   FusedLayout L{};
   const size_t A = static_cast<size_t>(T) * k;
+  L.rows_hint = local_rows_hint(T, k, E, n_local);
   L.y_dtype = ((flags & EIMOE_Y_F32) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
-  L.k_split = pick_down_split(static_cast<int>(A), n_local, H, I, static_cast<int>(elem_size(L.y_dtype)),
-                              (flags & EIMOE_W8A8) != 0);
+  L.k_split = pick_down_split(static_cast<int>(A), L.rows_hint, n_local, H, I,
+                              static_cast<int>(elem_size(L.y_dtype)), (flags & EIMOE_W8A8) != 0);
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -155,8 +180,9 @@ __global__ void dense_segment_kernel(int32_t* off, int T) {
 
 int run_gate_up(const void* a, const int32_t* a_rows, long long a_nrows, int lda, const void* w, int w_dtype,
                 const float* w_scale, int H, int I, const int32_t* seg, int n_seg, int e_mod, int max_rows, void* h,
-                int tile, hipStream_t s, const float* a_scale = nullptr) {
+                int tile, hipStream_t s, const float* a_scale = nullptr, int rows_hint = 0) {
   GemmArgs p{};
+  p.rows_hint = rows_hint;
   p.a = a;
   p.a_rows = a_rows;
   p.lda = lda;
@@ -184,8 +210,9 @@ int run_gate_up(const void* a, const int32_t* a_rows, long long a_nrows, int lda
 
 int run_down(const void* h, int I, const void* w, int w_dtype, const float* w_scale, int H, const int32_t* seg,
              int n_seg, int e_mod, int max_rows, void* y, int y_dtype, int k_split, int tile, hipStream_t s,
-             const float* h_scale = nullptr) {
+             const float* h_scale = nullptr, int rows_hint = 0) {
   GemmArgs p{};
+  p.rows_hint = rows_hint;
   p.a = h;
   p.a_rows = nullptr;
   p.lda = I;
@@ -492,7 +519,7 @@ size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_
                                        int out_dtype, int flags) {
   (void)E;
   if (T < 0 || H < 1 || I < 1 || k < 1 || n_local < 1 || shared_inter < 0) return 0;
-  return fused_layout(T, H, I, k, n_local, shared_inter, out_dtype, flags).total;
+  return fused_layout(T, H, I, E, k, n_local, shared_inter, out_dtype, flags).total;
 }
 
 int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int E, int k, const void* w_gate_up,
@@ -531,7 +558,7 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
     REQUIRE_PTR(shared_gate_up);
     REQUIRE_PTR(shared_down);
   }
-  const FusedLayout L = fused_layout(T, H, I, k, n_local, shared_inter, out_dtype, flags);
+  const FusedLayout L = fused_layout(T, H, I, E, k, n_local, shared_inter, out_dtype, flags);
   if (workspace_bytes < L.total)
     return fail(EIMOE_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -558,18 +585,18 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
     float* sh = static_cast<float*>(at(L.sh));
     if ((rc = hip_check(launch_quantize_rows_fp8(x, kBF16, T, H, xq, sx, s), "quantize x"))) return rc;
     if ((rc = run_gate_up(xq, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
-                          A, at(L.h), EIMOE_TILE_AUTO, s, sx)))
+                          A, at(L.h), EIMOE_TILE_AUTO, s, sx, L.rows_hint)))
       return rc;
     if ((rc = hip_check(launch_quantize_rows_fp8(at(L.h), kBF16, A, I, hq, sh, s), "quantize h"))) return rc;
     if ((rc = run_down(hq, I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y), L.y_dtype,
-                       L.k_split, EIMOE_TILE_AUTO, s, sh)))
+                       L.k_split, EIMOE_TILE_AUTO, s, sh, L.rows_hint)))
       return rc;
   } else {
     if ((rc = run_gate_up(x, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
-                          A, at(L.h), EIMOE_TILE_AUTO, s)))
+                          A, at(L.h), EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
       return rc;
     if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y),
-                       L.y_dtype, L.k_split, EIMOE_TILE_AUTO, s)))
+                       L.y_dtype, L.k_split, EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
       return rc;
   }
   const void* sh_y = nullptr;

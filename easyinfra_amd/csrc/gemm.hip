@@ -30,6 +30,8 @@
 //     c*NI + j, so each lane owns NI adjacent output columns and stores are wide.
 //   * SiLU epilogue: a tile holds gate rows [n0, n0+BN/2) and the matching up rows
 //     [I+n0, ...); h = silu(g)*u is formed in registers and stored as bf16.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -662,23 +664,42 @@ int gemm_out_cols_per_tile(int tile, int epi) {
   return epi == kEpiSiluBF16 ? bn / 2 : bn;
 }
 
-// Tile heuristic from the average rows per segment (the host knows only the bound).
-// Measured on the routed offsets of the workloads: the 256x256 tile matches or beats
-// 128x128 from ~256 rows per segment up (DeepSeek-V2-Lite 4096 tokens: 717 vs 710 us
-// skewed, 580 vs 657 us uniform, gate/up + down), and skewed loads put most rows in
-// a few large segments whatever the average.
-int gemm_pick_tile(int epi, int max_rows, int S, int N) {
-  const double avg = static_cast<double>(max_rows) / (S > 0 ? S : 1);
+// Tile heuristic (the host knows only the row bound, or a caller's estimate, and the shapes).
+// Measured on the routed offsets of the workloads (cold caches; us, gate/up + down):
+//  * experts of >= 32 MiB of weights (Mixtral-8x7B) are read from HBM once per row chunk of
+//    a segment, so the tile should cover a segment in one chunk.  64 tokens (16 rows per
+//    expert): bf16 gate/up streams (335 vs 372 with 32x128), the down projection takes
+//    128x128 with K split 2 (159 vs 178 streaming); e4m3 W8A8 takes 32x128 for both (180
+//    vs 190, 84 vs 97).  128-256 tokens (32-64 rows): 128x128 (gate/up 377 and 402 vs 478
+//    and 911 with 32x128).  From 128 rows: 256x256;
+//  * small experts (DeepSeek-V2-Lite, Qwen3 local share) stay in cache: gate/up keeps the
+//    256x256 tile from ~256 rows per segment of the bound (DeepSeek 4096 tokens 717 vs 710
+//    us skewed, 580 vs 657 uniform against 128x128); the down projection (short K) wants
+//    more, smaller tiles: 128x128 below ~384 expected rows per segment (Qwen3 2048 tokens:
+//    46 vs 62 us), 32x128 below ~96.
+int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
+  const int S = p.S > 0 ? p.S : 1;
+  const double avg_bound = static_cast<double>(p.max_rows) / S;
+  const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) / S;
+  const double expert_bytes = static_cast<double>(p.nb_rows) * p.K * p.k_split * (b_fp8 ? 1 : 2);
+  const bool silu = epi == kEpiSiluBF16;
   int t;
-  if (avg >= 256) {
+  if (expert_bytes >= 32.0 * 1024 * 1024) {
+    if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 128 ? kTileM : kTileL;
+    else if (silu) t = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    else t = avg < 8 ? kTileXS : avg < 128 ? kTileM : kTileL;
+  } else if (silu) {
+    t = avg_bound >= 256 ? kTileL : avg_bound >= 96 ? kTileM : avg_bound >= 24 ? kTileS : kTileXS;
+  } else {
+    t = avg < 6 ? kTileXS : avg < 96 ? kTileS : avg < 384 ? kTileM : kTileL;
+  }
+  if (t == kTileL) {
     // fewer 256x256 tiles than CUs (a dense shared-expert launch, say) leaves CUs idle: step down
-    const long long mt = static_cast<long long>(max_rows) / 256 + S;
-    t = (N % gemm_out_cols_per_tile(kTileL, epi) == 0 && mt * (N / gemm_out_cols_per_tile(kTileL, epi)) < kNumCu)
-            ? kTileM : kTileL;
-  } else if (avg >= 96) t = kTileM;
-  else if (avg >= 24) t = kTileS;
-  else t = kTileXS;
-  while (t != kTileXS && N % gemm_out_cols_per_tile(t, epi) != 0) ++t;
+    const long long mt = static_cast<long long>(p.max_rows) / 256 + S;
+    const int oc = gemm_out_cols_per_tile(kTileL, epi);
+    if (p.N % oc == 0 && mt * (p.N / oc) * p.k_split < kNumCu) t = kTileM;
+  }
+  while (t != kTileXS && p.N % gemm_out_cols_per_tile(t, epi) != 0) ++t;
   return t;
 }
 
@@ -689,7 +710,7 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
   // activations (W8A16) stay on the LDS-tiled kernels.
   const bool stream_ok = (b_fp8 == a_fp8) && stream_gemm_supported(p, epi, a_fp8);
   if (tile == kTileAuto) {
-    tile = gemm_pick_tile(epi, max_rows, p.S, p.N);
+    tile = gemm_pick_tile(p, epi, b_fp8);
     // a few rows per segment: stream the weights instead of tiling them through LDS
     if (tile == kTileXS && stream_ok) tile = kTileStream;
   }

@@ -34,6 +34,7 @@ struct GemmArgs {
   int max_rows;              // rows of A (non-gathered) / of C; segment bounds are clamped to it
   long long a_rows_cap;      // rows in the A buffer (bounds the buffer resource)
   const float* a_scale;      // fp8 A: per-row dequantisation scale, indexed like A (through a_rows)
+  int rows_hint;             // expected rows in the segments (tile choice only); 0: max_rows
 };
 
 // Tile shape selector; the launcher maps it to a kernel instantiation.
@@ -60,7 +61,9 @@ hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long spl
 // a_fp8: A and B are both fp8-e4m3 (W8A8 on the fp8 MFMA); b_fp8 alone: W8A16.
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
                                hipStream_t s);
-int gemm_pick_tile(int epi, int max_rows, int S, int N);
+// Tile for a launch: from the expected rows per segment, the output width and the bytes of
+// one expert's weights (rows_hint/max_rows, p.S, p.N, p.K * p.k_split, nb_rows).
+int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8);
 // Weight-streaming kernel (stream.hip) for segments of a few rows: bf16 x bf16, or
 // e4m3 x e4m3 (fp8 = true, W8A8 with p.a_scale / p.b_scale).
 bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8);
