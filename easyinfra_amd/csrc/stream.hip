@@ -319,11 +319,13 @@ hipError_t launch_stream_w(const GemmArgs& p, dim3 g, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Grid from the row bound; the K split from the expected rows (rows_hint) when given.
 template <int EPI, int NFRAG, int MBLK, bool FP8>
-hipError_t launch_stream_cfg(const GemmArgs& p, int max_rows, hipStream_t s) {
-  const long long tasks = stream_tasks_bound(p, max_rows, NFRAG, MBLK, EPI);
-  if (tasks > 0x7fffffffll) return hipErrorInvalidValue;
-  const dim3 g(static_cast<unsigned>(tasks > 0 ? tasks : 1));
+hipError_t launch_stream_cfg(const GemmArgs& p, int max_rows, int rows, hipStream_t s) {
+  const long long grid = stream_tasks_bound(p, max_rows, NFRAG, MBLK, EPI);
+  if (grid > 0x7fffffffll) return hipErrorInvalidValue;
+  const dim3 g(static_cast<unsigned>(grid > 0 ? grid : 1));
+  const long long tasks = stream_tasks_bound(p, rows, NFRAG, MBLK, EPI);
   // Split K over the workgroup's waves only while each wave keeps >= 16 steps: shorter
   // streams spend a large share of their time filling and draining the register ring.
   const int ks = p.K / (FP8 ? 128 : 64);
@@ -343,9 +345,9 @@ hipError_t launch_stream_cfg(const GemmArgs& p, int max_rows, hipStream_t s) {
 }
 
 template <int EPI, int NFRAG, bool FP8>
-hipError_t launch_stream_nf(const GemmArgs& p, int max_rows, int mblk, hipStream_t s) {
-  return mblk == 1 ? launch_stream_cfg<EPI, NFRAG, 1, FP8>(p, max_rows, s)
-                   : launch_stream_cfg<EPI, NFRAG, 2, FP8>(p, max_rows, s);
+hipError_t launch_stream_nf(const GemmArgs& p, int max_rows, int rows, int mblk, hipStream_t s) {
+  return mblk == 1 ? launch_stream_cfg<EPI, NFRAG, 1, FP8>(p, max_rows, rows, s)
+                   : launch_stream_cfg<EPI, NFRAG, 2, FP8>(p, max_rows, rows, s);
 }
 
 // Fragments per wave: as many as the output width allows, up to 8 (each activation load
@@ -376,13 +378,14 @@ int stream_out_cols(int N, int epi, bool fp8) {
 }
 
 hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s) {
-  const int nf = stream_nfrag(p, epi, max_rows, mblk, fp8);
+  const int rows = p.rows_hint > 0 ? std::min(p.rows_hint, max_rows) : max_rows;   // expected rows
+  const int nf = stream_nfrag(p, epi, rows, mblk, fp8);
   if (p.K % (fp8 ? 128 : 64) != 0 || nf == 0) return hipErrorInvalidValue;
 #define EIMOE_STREAM_NF(E, F8)                                               \
   switch (nf) {                                                              \
-    case 8: return launch_stream_nf<E, 8, F8>(p, max_rows, mblk, s);         \
-    case 4: return launch_stream_nf<E, 4, F8>(p, max_rows, mblk, s);         \
-    default: return launch_stream_nf<E, 2, F8>(p, max_rows, mblk, s);        \
+    case 8: return launch_stream_nf<E, 8, F8>(p, max_rows, rows, mblk, s);   \
+    case 4: return launch_stream_nf<E, 4, F8>(p, max_rows, rows, mblk, s);   \
+    default: return launch_stream_nf<E, 2, F8>(p, max_rows, rows, mblk, s);  \
   }
   if (fp8) {
     if (epi == kEpiSiluBF16) { EIMOE_STREAM_NF(kEpiSiluBF16, true) }
