@@ -37,6 +37,33 @@ int hip_check(hipError_t e, const char* what) {
 
 inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
 
+// A second stream per (host thread, device) with its fork/join events, created on first
+// use and kept until the process ends: the fused layer runs the shared experts on it so
+// their launches overlap the routed ones (each alone ends in a mostly idle CU round).
+// Default priority, non-blocking; the fork/join through events also holds under graph
+// capture of the caller's stream.
+struct AuxStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kMaxDevices = 64;
+
+hipError_t aux_stream(AuxStream** out) {
+  thread_local AuxStream aux[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  AuxStream& a = aux[dev];
+  if (!a.stream) {
+    if ((e = hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking)) != hipSuccess) return e;
+    if ((e = hipEventCreateWithFlags(&a.fork, hipEventDisableTiming)) != hipSuccess) return e;
+    if ((e = hipEventCreateWithFlags(&a.join, hipEventDisableTiming)) != hipSuccess) return e;
+  }
+  *out = &a;
+  return hipSuccess;
+}
+
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 int elem_size(int dt) { return dt == EIMOE_F32 ? 4 : dt == EIMOE_BF16 ? 2 : dt == EIMOE_FP8 ? 1 : 0; }
@@ -573,45 +600,73 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   const hipStream_t s = S(stream);
   const int A = T * k;
   int rc;
-  if ((rc = hip_check(launch_route_align(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, e_lo, n_local, ids, w,
-                                         counts, offsets, sorted_flat, sorted_tok, pos, s),
-                      "route_align")))
-    return rc;
-  if (flags & EIMOE_W8A8) {
-    // activations quantised per token (x) and per row (h); both GEMMs on the fp8 MFMA
-    uint8_t* xq = static_cast<uint8_t*>(at(L.xq));
-    float* sx = static_cast<float*>(at(L.sx));
-    uint8_t* hq = static_cast<uint8_t*>(at(L.hq));
-    float* sh = static_cast<float*>(at(L.sh));
-    if ((rc = hip_check(launch_quantize_rows_fp8(x, kBF16, T, H, xq, sx, s), "quantize x"))) return rc;
-    if ((rc = run_gate_up(xq, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
-                          A, at(L.h), EIMOE_TILE_AUTO, s, sx, L.rows_hint)))
-      return rc;
-    if ((rc = hip_check(launch_quantize_rows_fp8(at(L.h), kBF16, A, I, hq, sh, s), "quantize h"))) return rc;
-    if ((rc = run_down(hq, I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y), L.y_dtype,
-                       L.k_split, EIMOE_TILE_AUTO, s, sh, L.rows_hint)))
-      return rc;
-  } else {
-    if ((rc = run_gate_up(x, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
-                          A, at(L.h), EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
-      return rc;
-    if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y),
-                       L.y_dtype, L.k_split, EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
-      return rc;
-  }
+  // Shared experts (every token, weight 1) depend only on x: fork them onto the second
+  // stream first, so they run beside the routing and the routed GEMMs; joined before the
+  // combine.
   const void* sh_y = nullptr;
+  AuxStream* aux = nullptr;
   if (shared_inter > 0) {
-    int32_t* sh_off = static_cast<int32_t*>(at(L.sh_off));
-    hipLaunchKernelGGL(dense_segment_kernel, dim3(1), dim3(64), 0, s, sh_off, T);
-    if ((rc = hip_check(hipGetLastError(), "shared offsets"))) return rc;
-    if ((rc = run_gate_up(x, nullptr, T, H, shared_gate_up, EIMOE_BF16, nullptr, H, shared_inter, sh_off, 1, 1, T,
-                          at(L.sh_h), EIMOE_TILE_AUTO, s)))
-      return rc;
-    if ((rc = run_down(at(L.sh_h), shared_inter, shared_down, EIMOE_BF16, nullptr, H, sh_off, 1, 1, T, at(L.sh_y),
-                       L.y_dtype, 1, EIMOE_TILE_AUTO, s)))
-      return rc;
+    if ((rc = hip_check(aux_stream(&aux), "aux stream"))) return rc;
+    const hipStream_t s2 = aux->stream;
+    if ((rc = hip_check(hipEventRecord(aux->fork, s), "fork"))) return rc;
+    if ((rc = hip_check(hipStreamWaitEvent(s2, aux->fork, 0), "fork wait"))) return rc;
+    auto shared = [&]() -> int {
+      int rc;
+      int32_t* sh_off = static_cast<int32_t*>(at(L.sh_off));
+      hipLaunchKernelGGL(dense_segment_kernel, dim3(1), dim3(64), 0, s2, sh_off, T);
+      if ((rc = hip_check(hipGetLastError(), "shared offsets"))) return rc;
+      if ((rc = run_gate_up(x, nullptr, T, H, shared_gate_up, EIMOE_BF16, nullptr, H, shared_inter, sh_off, 1, 1, T,
+                            at(L.sh_h), EIMOE_TILE_AUTO, s2)))
+        return rc;
+      return run_down(at(L.sh_h), shared_inter, shared_down, EIMOE_BF16, nullptr, H, sh_off, 1, 1, T, at(L.sh_y),
+                      L.y_dtype, 1, EIMOE_TILE_AUTO, s2);
+    };
+    rc = shared();
+    const int rj = hip_check(hipEventRecord(aux->join, s2), "join");
+    if (rc || rj) {   // still make the caller's stream wait for whatever was launched
+      hipStreamWaitEvent(s, aux->join, 0);
+      return rc ? rc : rj;
+    }
     sh_y = at(L.sh_y);
   }
+  // Routed part; whatever it returns, the caller's stream then waits for the shared work
+  // (an early error return must not leave the second stream using the workspace unjoined).
+  auto routed = [&]() -> int {
+    int rc;
+    if ((rc = hip_check(launch_route_align(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, e_lo, n_local, ids, w,
+                                           counts, offsets, sorted_flat, sorted_tok, pos, s),
+                        "route_align")))
+      return rc;
+    if (flags & EIMOE_W8A8) {
+      // activations quantised per token (x) and per row (h); both GEMMs on the fp8 MFMA
+      uint8_t* xq = static_cast<uint8_t*>(at(L.xq));
+      float* sx = static_cast<float*>(at(L.sx));
+      uint8_t* hq = static_cast<uint8_t*>(at(L.hq));
+      float* sh = static_cast<float*>(at(L.sh));
+      if ((rc = hip_check(launch_quantize_rows_fp8(x, kBF16, T, H, xq, sx, s), "quantize x"))) return rc;
+      if ((rc = run_gate_up(xq, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
+                            A, at(L.h), EIMOE_TILE_AUTO, s, sx, L.rows_hint)))
+        return rc;
+      if ((rc = hip_check(launch_quantize_rows_fp8(at(L.h), kBF16, A, I, hq, sh, s), "quantize h"))) return rc;
+      if ((rc = run_down(hq, I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y), L.y_dtype,
+                         L.k_split, EIMOE_TILE_AUTO, s, sh, L.rows_hint)))
+        return rc;
+    } else {
+      if ((rc = run_gate_up(x, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
+                            A, at(L.h), EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
+        return rc;
+      if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y),
+                         L.y_dtype, L.k_split, EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
+        return rc;
+    }
+    return EIMOE_OK;
+  };
+  rc = routed();
+  if (aux) {
+    const int rj = hip_check(hipStreamWaitEvent(s, aux->join, 0), "join wait");
+    if (!rc) rc = rj;
+  }
+  if (rc) return rc;
   return hip_check(launch_combine(at(L.y), L.y_dtype, L.k_split, static_cast<long long>(A) * H, pos, w, T, k, H, sh_y,
                                   L.y_dtype, out, out_dtype, s),
                    "combine");
