@@ -48,14 +48,18 @@ struct AuxStream {
 };
 constexpr int kMaxDevices = 64;
 
-hipError_t aux_stream(AuxStream** out) {
+// *out stays null when the stream does not exist yet and may not be created now (the
+// caller's stream is capturing: creating a stream then would invalidate the capture).
+hipError_t aux_stream(AuxStream** out, bool may_create) {
   thread_local AuxStream aux[kMaxDevices];
+  *out = nullptr;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   AuxStream& a = aux[dev];
   if (!a.stream) {
+    if (!may_create) return hipSuccess;
     if ((e = hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking)) != hipSuccess) return e;
     if ((e = hipEventCreateWithFlags(&a.fork, hipEventDisableTiming)) != hipSuccess) return e;
     if ((e = hipEventCreateWithFlags(&a.join, hipEventDisableTiming)) != hipSuccess) return e;
@@ -606,10 +610,14 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   const void* sh_y = nullptr;
   AuxStream* aux = nullptr;
   if (shared_inter > 0) {
-    if ((rc = hip_check(aux_stream(&aux), "aux stream"))) return rc;
-    const hipStream_t s2 = aux->stream;
-    if ((rc = hip_check(hipEventRecord(aux->fork, s), "fork"))) return rc;
-    if ((rc = hip_check(hipStreamWaitEvent(s2, aux->fork, 0), "fork wait"))) return rc;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if ((rc = hip_check(hipStreamIsCapturing(s, &cap), "capture status"))) return rc;
+    if ((rc = hip_check(aux_stream(&aux, cap == hipStreamCaptureStatusNone), "aux stream"))) return rc;
+    const hipStream_t s2 = aux ? aux->stream : s;   // no second stream yet under capture: serial
+    if (aux) {
+      if ((rc = hip_check(hipEventRecord(aux->fork, s), "fork"))) return rc;
+      if ((rc = hip_check(hipStreamWaitEvent(s2, aux->fork, 0), "fork wait"))) return rc;
+    }
     auto shared = [&]() -> int {
       int rc;
       int32_t* sh_off = static_cast<int32_t*>(at(L.sh_off));
@@ -622,11 +630,14 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
                       L.y_dtype, 1, EIMOE_TILE_AUTO, s2);
     };
     rc = shared();
-    const int rj = hip_check(hipEventRecord(aux->join, s2), "join");
-    if (rc || rj) {   // still make the caller's stream wait for whatever was launched
-      hipStreamWaitEvent(s, aux->join, 0);
-      return rc ? rc : rj;
+    if (aux) {
+      const int rj = hip_check(hipEventRecord(aux->join, s2), "join");
+      if (rc || rj) {   // still make the caller's stream wait for whatever was launched
+        hipStreamWaitEvent(s, aux->join, 0);
+        return rc ? rc : rj;
+      }
     }
+    if (rc) return rc;
     sh_y = at(L.sh_y);
   }
   // Routed part; whatever it returns, the caller's stream then waits for the shared work
