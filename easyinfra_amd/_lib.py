@@ -6,7 +6,7 @@ fallback: if it is missing, every op raises.
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_int, c_longlong, c_size_t, c_void_p, c_char_p, POINTER
+from ctypes import c_int, c_float, c_longlong, c_size_t, c_void_p, c_char_p, POINTER
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libeimoe.so")
@@ -14,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libeimoe.so")
 EIMOE_OK = 0
 ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_WORKSPACE, ERR_HIP = -1, -2, -3, -4, -5, -6
 F32, BF16, FP8 = 0, 1, 2
-RENORMALIZE, Y_F32, W8A8 = 1, 2, 4
+RENORMALIZE, Y_F32, W8A8, ROUTING_IN = 1, 2, 4, 8
 TILE_AUTO, TILE_256x256, TILE_128x128, TILE_32x128, TILE_16x64, TILE_STREAM = 0, 1, 2, 3, 4, 5
 MAX_TOPK, MAX_EXPERTS, MAX_SEGMENTS = 32, 512, 1024
 
@@ -26,6 +26,8 @@ SIGNATURES = {
     "eimoe_abi_version": (c_int, []),
     "eimoe_last_error": (c_char_p, []),
     "eimoe_router_topk": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "eimoe_router_grouped_topk": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int, c_float,
+                                          c_void_p, c_void_p, c_void_p]),
     "eimoe_align": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                             c_void_p, c_void_p]),
     "eimoe_route_align": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,

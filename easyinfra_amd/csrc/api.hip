@@ -292,6 +292,26 @@ int eimoe_router_topk(const float* logits, int T, int E, int k, int renormalize,
                    "router_topk");
 }
 
+int eimoe_router_grouped_topk(const float* logits, int T, int E, int k, int n_group, int topk_group,
+                              const float* bias, int renormalize, float scaling, int32_t* topk_ids,
+                              float* topk_weights, void* stream) {
+  if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
+  if (E < 2 || E > EIMOE_MAX_EXPERTS) return fail(EIMOE_ERR_SHAPE, "E=%d outside [2,%d]", E, EIMOE_MAX_EXPERTS);
+  if (k < 1 || k > E || k > EIMOE_MAX_TOPK)
+    return fail(EIMOE_ERR_SHAPE, "k=%d outside [1,min(E=%d,%d)]", k, E, EIMOE_MAX_TOPK);
+  if (n_group < 1 || E % n_group || E / n_group < 2)
+    return fail(EIMOE_ERR_SHAPE, "n_group=%d must divide E=%d into groups of >= 2 experts", n_group, E);
+  if (topk_group < 1 || topk_group > n_group)
+    return fail(EIMOE_ERR_SHAPE, "topk_group=%d outside [1,n_group=%d]", topk_group, n_group);
+  if (T == 0) return EIMOE_OK;
+  REQUIRE_PTR(logits);
+  REQUIRE_PTR(topk_ids);
+  REQUIRE_PTR(topk_weights);
+  return hip_check(launch_router_grouped(logits, T, E, k, n_group, topk_group, bias, renormalize ? 1 : 0, scaling,
+                                         topk_ids, topk_weights, S(stream)),
+                   "router_grouped_topk");
+}
+
 int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, int32_t* counts, int32_t* offsets,
                 int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream) {
   if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
@@ -575,8 +595,14 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   if ((flags & EIMOE_W8A8) && (H % 128 || I % 128))
     return fail(EIMOE_ERR_ALIGN, "W8A8 needs H=%d and I=%d multiples of 128", H, I);
   if (T == 0) return EIMOE_OK;
+  const bool routing_in = (flags & EIMOE_ROUTING_IN) != 0;
   REQUIRE_PTR(x);
-  REQUIRE_PTR(logits);
+  if (routing_in) {
+    REQUIRE_PTR(topk_ids_out);
+    REQUIRE_PTR(topk_w_out);
+  } else {
+    REQUIRE_PTR(logits);
+  }
   REQUIRE_PTR(w_gate_up);
   REQUIRE_PTR(w_down);
   REQUIRE_PTR(out);
@@ -644,10 +670,15 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   // (an early error return must not leave the second stream using the workspace unjoined).
   auto routed = [&]() -> int {
     int rc;
-    if ((rc = hip_check(launch_route_align(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, e_lo, n_local, ids, w,
-                                           counts, offsets, sorted_flat, sorted_tok, pos, s),
-                        "route_align")))
+    if (routing_in) {
+      if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos, s),
+                          "align")))
+        return rc;
+    } else if ((rc = hip_check(launch_route_align(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, e_lo,
+                                                  n_local, ids, w, counts, offsets, sorted_flat, sorted_tok, pos, s),
+                               "route_align"))) {
       return rc;
+    }
     if (flags & EIMOE_W8A8) {
       // activations quantised per token (x) and per row (h); both GEMMs on the fp8 MFMA
       uint8_t* xq = static_cast<uint8_t*>(at(L.xq));

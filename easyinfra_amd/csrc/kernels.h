@@ -42,6 +42,10 @@ enum TileCfg : int { kTileAuto = 0, kTileL = 1, kTileM = 2, kTileS = 3, kTileXS 
 
 hipError_t launch_router_topk(const float* logits, int T, int E, int k, int renorm, int32_t* ids, float* w,
                               hipStream_t s);
+// DeepSeek-V3 grouped top-k router (sigmoid, correction bias, group-limited), E <= 512.
+hipError_t launch_router_grouped(const float* logits, int T, int E, int k, int n_group, int topk_group,
+                                 const float* bias, int renorm, float scaling, int32_t* ids, float* w,
+                                 hipStream_t s);
 size_t align_lds_bytes(int n_loc);
 hipError_t launch_align(const int32_t* ids, int T, int k, int e_lo, int n_loc, int32_t* counts, int32_t* offsets,
                         int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, hipStream_t s);

@@ -50,6 +50,171 @@ hipError_t launch_router_topk(const float* logits, int T, int E, int k, int reno
   return launch_router_lv<64, 8>(logits, T, E, k, renorm, ids, w, s);
 }
 
+// ---------------------------------------------------------------------------- grouped
+// DeepSeek-V3 gate, "noaux_tc" (DeepseekV3MoEGate.forward, models/deepseek_v3/
+// modeling_deepseek_v3.py:151-203), on precomputed fp32 logits:
+//   s = sigmoid(logits); c = s + bias;
+//   group score = sum of the top 2 of c inside each of n_group equal expert groups;
+//   keep the topk_group best groups, c := 0 outside them (masked_fill 0.0, not -inf);
+//   ids = top-k of c; w = s[ids]; w /= sum(w) + 1e-20 when renormalising (k > 1);
+//   w *= scaling.
+// Selection depends on how s rounds (the bias breaks the monotonicity that lets the
+// softmax router compare logits), so s is computed in double and rounded once to fp32:
+// the correctly rounded sigmoid, which the oracle computes the same way.  Ties go to the
+// lower group / expert id; the picks come out in descending order of c.
+// One wave per token (kGroupedWaves per workgroup); lane l holds experts l*VPL..+VPL-1.
+// Group scores and group selection go through LDS, so any n_group dividing E works.
+constexpr int kGroupedWaves = 4;
+constexpr int kGroupedMaxE = 512;
+
+__device__ __forceinline__ float sigmoid_rn(float x) {
+  return static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(x))));
+}
+
+__device__ __forceinline__ void top2_insert(float v, float& a1, float& a2) {
+  if (v > a1) {
+    a2 = a1;
+    a1 = v;
+  } else if (v > a2) {
+    a2 = v;
+  }
+}
+
+template <int VPL>
+__global__ __launch_bounds__(64 * kGroupedWaves) void router_grouped_kernel(
+    const float* __restrict__ logits, int T, int E, int k, int n_group, int topk_group, const float* __restrict__ bias,
+    int renorm, float scaling, int32_t* __restrict__ ids, float* __restrict__ wts) {
+  __shared__ float s_gs[kGroupedWaves][kGroupedMaxE / 2];   // group scores (groups hold >= 2 experts)
+  __shared__ int s_sel[kGroupedWaves][kGroupedMaxE / 2];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int t = blockIdx.x * kGroupedWaves + wv;
+  if (t >= T) return;   // wave-uniform; no barrier below
+  const float NEG_INF = -__builtin_inff();
+  const int gsize = E / n_group;
+
+  float sg[VPL], c[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane * VPL + j;
+    if (e < E) {
+      sg[j] = sigmoid_rn(logits[static_cast<long long>(t) * E + e]);
+      c[j] = sg[j] + (bias ? bias[e] : 0.f);
+    } else {
+      sg[j] = 0.f;
+      c[j] = NEG_INF;
+    }
+  }
+  // group scores: top-2 sum per group, one wave-wide reduction per group
+#pragma unroll 1
+  for (int g = 0; g < n_group; ++g) {
+    float a1 = NEG_INF, a2 = NEG_INF;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int e = lane * VPL + j;
+      if (e < E && e / gsize == g) top2_insert(c[j], a1, a2);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float b1 = __shfl_xor(a1, m, 64);
+      const float b2 = __shfl_xor(a2, m, 64);
+      const float hi = fmaxf(a1, b1);
+      a2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
+      a1 = hi;
+    }
+    if (lane == 0) s_gs[wv][g] = a1 + a2;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // keep the topk_group best groups (ties to the lower group index)
+  for (int g = lane; g < n_group; g += 64) {
+    const float v = s_gs[wv][g];
+    int rank = 0;
+    for (int h = 0; h < n_group; ++h) {
+      const float u = s_gs[wv][h];
+      rank += (u > v || (u == v && h < g)) ? 1 : 0;
+    }
+    s_sel[wv][g] = rank < topk_group;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  uint32_t avail = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane * VPL + j;
+    if (e < E) {
+      if (!s_sel[wv][e / gsize]) c[j] = 0.f;
+      avail |= 1u << j;
+    }
+  }
+  // top-k of the masked scores; pick r is kept by lane r (k <= 32)
+  int my_id = -1;
+#pragma unroll 1
+  for (int r = 0; r < k; ++r) {
+    float bv = NEG_INF;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int e = lane * VPL + j;
+      if (((avail >> j) & 1u) && (c[j] > bv || (c[j] == bv && e < bi))) {
+        bv = c[j];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float ov = __shfl_xor(bv, m, 64);
+      const int oi = __shfl_xor(bi, m, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == r) my_id = bi;
+    if (bi / VPL == lane) avail &= ~(1u << (bi % VPL));
+  }
+  // weight = unbiased sigmoid of the pick, fetched from its owner lane
+  float w = 0.f;
+  const int src = my_id >= 0 ? my_id / VPL : 0;
+  const int jj = my_id >= 0 ? my_id % VPL : 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const float v = __shfl(sg[j], src, 64);
+    if (j == jj) w = v;
+  }
+  if (lane >= k) w = 0.f;
+  if (renorm && k > 1) {
+    float sum = w;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+    w = w / (sum + 1e-20f);
+  }
+  w = w * scaling;
+  if (lane < k) {
+    ids[static_cast<long long>(t) * k + lane] = my_id;
+    wts[static_cast<long long>(t) * k + lane] = w;
+  }
+}
+
+hipError_t launch_router_grouped(const float* logits, int T, int E, int k, int n_group, int topk_group,
+                                 const float* bias, int renorm, float scaling, int32_t* ids, float* w,
+                                 hipStream_t s) {
+  const unsigned blocks = static_cast<unsigned>((T + kGroupedWaves - 1) / kGroupedWaves);
+  const dim3 g(blocks > 0 ? blocks : 1), b(64 * kGroupedWaves);
+  const int vpl = (E + 63) / 64;
+#define EIMOE_RG(V) \
+  hipLaunchKernelGGL((router_grouped_kernel<V>), g, b, 0, s, logits, T, E, k, n_group, topk_group, bias, renorm, \
+                     scaling, ids, w)
+  if (vpl <= 1) EIMOE_RG(1);
+  else if (vpl <= 2) EIMOE_RG(2);
+  else if (vpl <= 4) EIMOE_RG(4);
+  else EIMOE_RG(8);
+#undef EIMOE_RG
+  return hipGetLastError();
+}
+
 // Router and align in one workgroup, for batches its 16 waves route in a few steps: the
 // ids stay in LDS between the two phases, and one launch (a few microseconds of dispatch
 // and cold-cache latency at decode sizes) replaces two.  Same outputs as the two kernels.

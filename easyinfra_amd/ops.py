@@ -54,6 +54,24 @@ def router_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True) -> T
     return ids, w
 
 
+def router_grouped_topk(logits: torch.Tensor, top_k: int, n_group: int = 1, topk_group: int = 1,
+                        bias: Optional[torch.Tensor] = None, renormalize: bool = True,
+                        scaling: float = 1.0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """DeepseekV3MoEGate.forward, "noaux_tc" (modeling_deepseek_v3.py:151-203) from the logits on
+    -> (ids int32 [T,k], weights fp32 [T,k])."""
+    _req(logits, "logits", torch.float32, 2)
+    T, E = logits.shape
+    if bias is not None:
+        _req(bias, "bias", torch.float32, 1)
+        if bias.numel() != E:
+            raise ValueError(f"bias has {bias.numel()} entries, logits {E} experts")
+    ids = torch.empty(T, top_k, dtype=torch.int32, device=logits.device)
+    w = torch.empty(T, top_k, dtype=torch.float32, device=logits.device)
+    call("eimoe_router_grouped_topk", logits.data_ptr(), T, E, top_k, n_group, topk_group, _ptr(bias),
+         int(renormalize), float(scaling), ids.data_ptr(), w.data_ptr(), _stream(logits))
+    return ids, w
+
+
 def align(topk_ids: torch.Tensor, n_local: int, e_lo: int = 0) -> dict:
     """Counts/offsets/stable permutation (blocks/moe/base.py:343-364, moe_all2all.py:346-348)."""
     _req(topk_ids, "topk_ids", torch.int32, 2)
@@ -249,7 +267,10 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
               w_down: torch.Tensor, *, renormalize: bool = True, shared_gate_up: Optional[torch.Tensor] = None,
               shared_down: Optional[torch.Tensor] = None, expert_range: Optional[Sequence[int]] = None,
               w_scales: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, out_dtype=None, y_fp32: bool = False,
-              w8a8: bool = False, workspace: Optional[torch.Tensor] = None, return_routing: bool = False):
+              w8a8: bool = False, workspace: Optional[torch.Tensor] = None, return_routing: bool = False,
+              scoring_func: str = "softmax", n_group: int = 1, topk_group: int = 1,
+              e_score_correction_bias: Optional[torch.Tensor] = None, routed_scaling_factor: float = 1.0,
+              routing: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, num_experts: Optional[int] = None):
     """The MoE layer: (hidden_states [T,H], router_logits [T,E], top_k) -> combined output [T,H].
 
     Reproduces MoeAll2AllBlock's stages at ep=1 (moe_all2all.py:85-95) with
@@ -264,17 +285,31 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     the bf16 MFMA (W8A16), or with ``w8a8=True`` activations quantised per token / per row
     and both GEMMs on the fp8 MFMA (W8A8).
     fp32 hidden states are rounded to bf16 for the MFMA path.
+    ``scoring_func="sigmoid"`` routes with the DeepSeek-V3 gate (``router_grouped_topk``:
+    ``n_group``, ``topk_group``, ``e_score_correction_bias``, ``routed_scaling_factor``,
+    ``renormalize`` as norm_topk_prob) instead of softmax top-k.  ``routing=(ids int32 [T,k],
+    weights fp32 [T,k])`` skips the router altogether (``router_logits`` may then be None, with
+    ``num_experts`` giving E when it is not the top of ``expert_range``).
     """
     x = hidden_states
     if x.dtype == torch.float32:
         x = x.to(torch.bfloat16)
     _req(x, "hidden_states", torch.bfloat16, 2)
-    _req(router_logits, "router_logits", torch.float32, 2)
+    if scoring_func not in ("softmax", "sigmoid"):
+        raise ValueError(f"scoring_func {scoring_func!r}: 'softmax' or 'sigmoid'")
+    if scoring_func == "sigmoid" and routing is None:
+        routing = router_grouped_topk(router_logits, top_k, n_group, topk_group, e_score_correction_bias,
+                                      renormalize, routed_scaling_factor)
+    if routing is None or router_logits is not None:
+        _req(router_logits, "router_logits", torch.float32, 2)
     _req(w_gate_up, "w_gate_up", (torch.bfloat16, torch.float8_e4m3fn), 3)
     _req(w_down, "w_down", (torch.bfloat16, torch.float8_e4m3fn), 3)
     T, H = x.shape
-    E = router_logits.shape[1]
     n_local, I2, H2 = w_gate_up.shape
+    if router_logits is not None:
+        E = router_logits.shape[1]
+    else:
+        E = num_experts or (expert_range[1] if expert_range is not None else n_local)
     I = I2 // 2
     if H2 != H or tuple(w_down.shape) != (n_local, H, I):
         raise ValueError(f"weight shapes {tuple(w_gate_up.shape)}/{tuple(w_down.shape)} do not match H={H}")
@@ -293,16 +328,25 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     if w8a8 and not fp8:
         raise ValueError("w8a8 needs fp8 weights and w_scales")
     flags = (_lib.RENORMALIZE if renormalize else 0) | (_lib.Y_F32 if y_fp32 else 0) | (_lib.W8A8 if w8a8 else 0)
+    if routing is not None:
+        ids_in, w_in = routing
+        _req(ids_in, "routing ids", torch.int32, 2)
+        _req(w_in, "routing weights", torch.float32, 2)
+        if tuple(ids_in.shape) != (T, top_k) or tuple(w_in.shape) != (T, top_k):
+            raise ValueError(f"routing tensors must be [T={T}, k={top_k}]")
+        flags |= _lib.ROUTING_IN
     need = fused_moe_workspace_bytes(T, H, I, E, top_k, n_local, Is, out_dtype, flags)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
     out = torch.empty(T, H, dtype=out_dtype, device=x.device)
     ids = w = None
-    if return_routing:
+    if routing is not None:
+        ids, w = routing
+    elif return_routing:
         ids = torch.empty(T, top_k, dtype=torch.int32, device=x.device)
         w = torch.empty(T, top_k, dtype=torch.float32, device=x.device)
     s_gu, s_d = w_scales if fp8 else (None, None)
-    call("eimoe_fused_moe", x.data_ptr(), router_logits.data_ptr(), T, H, I, E, top_k, w_gate_up.data_ptr(),
+    call("eimoe_fused_moe", x.data_ptr(), _ptr(router_logits), T, H, I, E, top_k, w_gate_up.data_ptr(),
          w_down.data_ptr(), _dt(w_gate_up), _ptr(s_gu), _ptr(s_d), lo, n_local, _ptr(shared_gate_up),
          _ptr(shared_down), Is, flags, out.data_ptr(), _DT[out_dtype], workspace.data_ptr(), workspace.numel(),
          _ptr(ids), _ptr(w), _stream(x))

@@ -45,7 +45,9 @@ enum { EIMOE_F32 = 0, EIMOE_BF16 = 1, EIMOE_FP8 = 2 };
 enum {
   EIMOE_RENORMALIZE = 1, /* renormalise the top-k weights (norm_topk_prob) */
   EIMOE_Y_F32 = 2,       /* keep the per-assignment expert outputs in fp32 (default: output dtype) */
-  EIMOE_W8A8 = 4         /* fp8 weights: also quantise activations per token and run the fp8 MFMA */
+  EIMOE_W8A8 = 4,        /* fp8 weights: also quantise activations per token and run the fp8 MFMA */
+  EIMOE_ROUTING_IN = 8   /* topk_ids / topk_w are inputs (routing done by the caller, e.g. with
+                            eimoe_router_grouped_topk); logits are not read and may be NULL */
 };
 
 /* tile selector for the GEMM entry points (0 = automatic).  EIMOE_TILE_STREAM is the
@@ -68,6 +70,20 @@ const char* eimoe_last_error(void);
  * topk_weights [T,k] fp32.  1 <= k <= min(E, EIMOE_MAX_TOPK), E <= EIMOE_MAX_EXPERTS. */
 int eimoe_router_topk(const float* logits, int T, int E, int k, int renormalize, int32_t* topk_ids,
                       float* topk_weights, void* stream);
+
+/* DeepSeek-V3 router, "noaux_tc" grouped top-k: DeepseekV3MoEGate.forward
+ * (models/deepseek_v3/modeling_deepseek_v3.py:151-203) from its logits on.
+ *   s = sigmoid(logits) (correctly rounded fp32); c = s + bias (bias [E] or NULL for zeros);
+ *   group score = sum of the 2 largest c in each of n_group equal groups of experts;
+ *   the topk_group best groups are kept and c is set to 0 elsewhere;
+ *   topk_ids = top-k of c (descending c, ties to the lower id);
+ *   topk_weights = s[ids], divided by their sum + 1e-20 when renormalize and k > 1, times scaling.
+ * logits [T,E] fp32 -> topk_ids [T,k] int32, topk_weights [T,k] fp32 (the reference casts the
+ * weights to the activation dtype; they stay fp32 here).  E <= EIMOE_MAX_EXPERTS, E % n_group == 0,
+ * E / n_group >= 2, 1 <= topk_group <= n_group, 1 <= k <= min(E, EIMOE_MAX_TOPK). */
+int eimoe_router_grouped_topk(const float* logits, int T, int E, int k, int n_group, int topk_group,
+                              const float* bias, int renormalize, float scaling, int32_t* topk_ids,
+                              float* topk_weights, void* stream);
 
 /* Align: per-expert counts, offsets and the stable expert-major permutation.
  * Replaces _MoeBlock._all_expert_count_compute (generation/blocks/moe/base.py:343-364) and the
@@ -171,7 +187,8 @@ size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_
  *   (bf16 or fp8 with per-channel scales [n_local,2I] / [n_local,H]); experts e_lo..e_lo+n_local-1
  *   of the router's E are resident (pass 0, E for a whole layer); shared experts optional
  *   (shared_gate_up [2*Is,H], shared_down [H,Is] bf16, weight 1.0); out [T,H] in out_dtype.
- * Optional outputs (may be NULL): topk_ids_out [T,k] int32, topk_w_out [T,k] fp32. */
+ * Optional outputs (may be NULL): topk_ids_out [T,k] int32, topk_w_out [T,k] fp32; with
+ * EIMOE_ROUTING_IN both are required inputs instead and the router is skipped. */
 int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int E, int k, const void* w_gate_up,
                     const void* w_down, int w_dtype, const float* w_gate_up_scale, const float* w_down_scale, int e_lo,
                     int n_local, const void* shared_gate_up, const void* shared_down, int shared_inter, int flags,

@@ -11,6 +11,8 @@ with every collective replaced by the identity it is at group size 1
 (easyinfra/generation/parallel/communicator.py:143-148, 168-172, 270-271):
 
   route_topk     modeling_qwen3_moe.py:255-266 (softmax -> top-k -> renorm)
+  route_grouped_topk  modeling_deepseek_v3.py:151-203 (DeepSeek-V3 gate: sigmoid,
+                 correction bias, group-limited top-k, renorm, scaling)
   align          blocks/moe/base.py:343-364 (per-expert counts),
                  moe_all2all.py:346-348 (sort, token index, slot), with the
                  EP-local expert window of blocks/moe/base.py:162-169, 187
@@ -66,6 +68,60 @@ def route_topk(logits: torch.Tensor, k: int, renormalize: bool = True) -> Tuple[
     if renormalize:
         w = w / w.sum(dim=-1, keepdim=True)
     return ids.to(torch.int32), w
+
+
+def sigmoid_rn(logits) -> np.ndarray:
+    """fp32 sigmoid rounded once from float64: the correctly rounded value (barring a float64
+    result within its own error of an fp32 rounding boundary)."""
+    x = np.asarray(logits, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return (1.0 / (1.0 + np.exp(-x))).astype(np.float32)
+
+
+def route_grouped_topk(logits, k: int, n_group: int, topk_group: int, bias=None, renormalize: bool = True,
+                       scaling: float = 1.0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """DeepseekV3MoEGate.forward with topk_method "noaux_tc" and scoring "sigmoid"
+    (modeling_deepseek_v3.py:151-203), from the fp32 logits on:
+
+      scores = sigmoid(logits)                                   (:157-158)
+      c = scores + e_score_correction_bias                       (:167)
+      group score = sum of the top 2 of c in each group          (:168-170)
+      keep topk_group groups; c := 0 outside them (masked_fill)  (:171-186)
+      ids = top-k of c; w = scores[ids]                          (:187-190)
+      w /= w.sum() + 1e-20 when norm_topk_prob and k > 1          (:196-198)
+      w *= routed_scaling_factor                                 (:199)
+
+    Deliberate choices where the reference is not reproducible: the sigmoid is the
+    correctly rounded fp32 value (``sigmoid_rn``; the reference's fp32 ``torch.sigmoid``
+    can differ by an ulp, which changes a pick only at an exact near-tie); both top-k
+    steps use ``sorted=False`` in the reference, so their tie order is implementation
+    defined: here groups and experts tie to the lower index, and the picks are listed
+    in descending order of c.  Weights stay fp32 (the reference casts them to the
+    activation dtype).  Returns (ids int32 [T,k], w fp32 [T,k]).
+    """
+    lg = np.asarray(torch.as_tensor(logits).float())
+    T, E = lg.shape
+    gsize = E // n_group
+    s = sigmoid_rn(lg)
+    b = np.zeros(E, np.float32) if bias is None else np.asarray(torch.as_tensor(bias).float())
+    c = (s + b[None, :]).astype(np.float32)
+    grp = np.sort(c.reshape(T, n_group, gsize), axis=-1)
+    gscore = (grp[..., -1] + grp[..., -2]).astype(np.float32)          # top-1 + top-2, fp32
+    keys = np.arange(n_group)
+    ids = np.zeros((T, k), np.int64)
+    w = np.zeros((T, k), np.float32)
+    for t in range(T):
+        gorder = sorted(keys, key=lambda g: (-float(gscore[t, g]), g))
+        keep = np.zeros(n_group, bool)
+        keep[gorder[:topk_group]] = True
+        cm = np.where(np.repeat(keep, gsize), c[t], np.float32(0.0))
+        order = sorted(range(E), key=lambda e: (-float(cm[e]), e))[:k]
+        ids[t] = order
+        w[t] = s[t, order]
+    if renormalize and k > 1:
+        w = (w / (w.sum(axis=-1, keepdims=True, dtype=np.float32) + np.float32(1e-20))).astype(np.float32)
+    w = (w * np.float32(scaling)).astype(np.float32)
+    return torch.from_numpy(ids.astype(np.int32)), torch.from_numpy(w)
 
 
 # --------------------------------------------------------------------------- align
@@ -140,13 +196,15 @@ def moe_forward(x: torch.Tensor, logits: torch.Tensor, k: int, w_gate_up: torch.
                 w_down: torch.Tensor, renormalize: bool = True,
                 shared_gate_up: Optional[torch.Tensor] = None, shared_down: Optional[torch.Tensor] = None,
                 expert_range: Optional[Tuple[int, int]] = None, round_h_bf16: bool = False,
-                token_subset: Optional[torch.Tensor] = None, return_parts: bool = False):
+                token_subset: Optional[torch.Tensor] = None, return_parts: bool = False,
+                routing: Optional[Tuple[torch.Tensor, torch.Tensor]] = None):
     """The layer at ep=1 (moe_all2all.py:85-95): route -> align -> gather -> experts -> combine.
 
     ``expert_range=(lo,hi)`` keeps only assignments to experts [lo,hi) (one GPU's EP
     share, blocks/moe/base.py:162-169); ``w_gate_up/w_down`` then hold those experts
     only.  Tokens with no local expert produce zero rows.  ``token_subset`` evaluates
     only the given token rows (the layer is row-independent given the logits).
+    ``routing=(ids, w)`` replaces the softmax router (e.g. with ``route_grouped_topk``).
     Returns fp32 [T or |subset|, H].
     """
     x = torch.as_tensor(x)
@@ -154,8 +212,10 @@ def moe_forward(x: torch.Tensor, logits: torch.Tensor, k: int, w_gate_up: torch.
     if token_subset is not None:
         token_subset = torch.as_tensor(token_subset, dtype=torch.long)
         x, logits = x[token_subset], logits[token_subset]
+        if routing is not None:
+            routing = (routing[0][token_subset], routing[1][token_subset])
     T, H = x.shape
-    ids, w = route_topk(logits, k, renormalize)
+    ids, w = routing if routing is not None else route_topk(logits, k, renormalize)
     lo, hi = expert_range if expert_range is not None else (0, w_gate_up.shape[0])
     al = align(ids.numpy(), hi - lo, lo)
     out = torch.zeros(T, H, dtype=torch.float32)

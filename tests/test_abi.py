@@ -65,6 +65,17 @@ def test_route_align_validation():
     assert _rc("eimoe_route_align", None, 4, 8, 2, 1, 0, 8, *n, None) == _lib.ERR_NULL
 
 
+def test_router_grouped_validation():
+    f = "eimoe_router_grouped_topk"
+    assert _rc(f, None, 4, 256, 8, 7, 4, None, 1, 1.0, None, None, None) == _lib.ERR_SHAPE    # 7 does not divide 256
+    assert _rc(f, None, 4, 8, 2, 8, 4, None, 1, 1.0, None, None, None) == _lib.ERR_SHAPE      # groups of 1 expert
+    assert _rc(f, None, 4, 256, 8, 8, 9, None, 1, 1.0, None, None, None) == _lib.ERR_SHAPE    # topk_group > n_group
+    assert _rc(f, None, 4, 256, 33, 8, 4, None, 1, 1.0, None, None, None) == _lib.ERR_SHAPE   # k > 32
+    assert _rc(f, None, 4, 1024, 8, 8, 4, None, 1, 1.0, None, None, None) == _lib.ERR_SHAPE   # E > 512
+    assert _rc(f, None, 4, 256, 8, 8, 4, None, 1, 1.0, None, None, None) == _lib.ERR_NULL
+    assert _rc(f, None, 0, 256, 8, 8, 4, None, 1, 1.0, None, None, None) == _lib.EIMOE_OK
+
+
 def test_gemm_validation():
     # H not a multiple of 64
     assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 100, 1, _lib.BF16, None, 100, 64, 1, 1, 1, 4, 1, 0,

@@ -57,6 +57,39 @@ def test_router_empty(dev):
     assert ids.shape == (0, 2) and w.shape == (0, 2)
 
 
+# --------------------------------------------------------------------------- DeepSeek-V3 gate
+@pytest.mark.parametrize("T,E,k,ng,tg,norm,scale,use_bias", [
+    (1, 256, 8, 8, 4, True, 2.5, True), (300, 256, 8, 8, 4, True, 2.5, True), (257, 64, 6, 1, 1, True, 2.446, False),
+    (33, 512, 32, 256, 16, True, 1.5, True), (5, 16, 3, 4, 2, False, 2.5, True), (40, 100, 6, 10, 3, True, 1.0, True),
+    (7, 8, 8, 4, 4, True, 1.0, False)])
+def test_router_grouped_matches_oracle(dev, T, E, k, ng, tg, norm, scale, use_bias):
+    g = torch.Generator().manual_seed(T * 7 + E)
+    logits = torch.randn(T, E, generator=g) * 2.0
+    bias = torch.randn(E, generator=g) * 0.1 if use_bias else None
+    ids, w = ops.router_grouped_topk(logits.to(dev), k, ng, tg, None if bias is None else bias.to(dev), norm, scale)
+    rid, rw = oracle.route_grouped_topk(logits, k, ng, tg, bias, norm, scale)
+    assert torch.equal(cpu(ids), rid)
+    torch.testing.assert_close(cpu(w), rw, rtol=2e-6, atol=1e-7)
+
+
+def test_router_grouped_ties_and_masked_zeros(dev):
+    # integer logits: equal scores everywhere (ties to the lower group / expert); the second
+    # row makes every kept score negative so experts masked to 0.0 are picked
+    logits = torch.tensor([[1., 1., 2., 2., 1., 1., 2., 2., 0., 0., 0., 0., 2., 2., 1., 1.],
+                           [-4.] * 16])
+    bias = torch.cat([torch.zeros(16)]) - 0.5
+    for ng, tg, k in [(4, 2, 3), (8, 1, 5), (2, 1, 4)]:
+        ids, w = ops.router_grouped_topk(logits.to(dev), k, ng, tg, bias.to(dev), True, 1.0)
+        rid, rw = oracle.route_grouped_topk(logits, k, ng, tg, bias, True, 1.0)
+        assert torch.equal(cpu(ids), rid), (ng, tg, k)
+        torch.testing.assert_close(cpu(w), rw, rtol=2e-6, atol=1e-7)
+
+
+def test_router_grouped_empty(dev):
+    ids, w = ops.router_grouped_topk(torch.empty(0, 64, device=dev), 6, 8, 4)
+    assert ids.shape == (0, 6)
+
+
 # --------------------------------------------------------------------------- align
 @pytest.mark.parametrize("T,k,E,e_lo,n_loc,skew", [
     (1, 2, 8, 0, 8, False), (512, 2, 8, 0, 8, False), (8192, 2, 8, 0, 8, False), (4096, 6, 64, 0, 64, True),

@@ -91,6 +91,32 @@ def test_layer_no_local_expert_rows_are_zero(dev):
     assert torch.count_nonzero(cpu(out)[~local]) == 0
 
 
+@pytest.mark.parametrize("T", [1, 77])
+def test_layer_deepseek_v3_gate(dev, T):
+    """The layer routed by the DeepSeek-V3 gate (sigmoid, correction bias, 8 groups keep 4,
+    routed_scaling_factor) with shared experts, against the oracle on the same routing."""
+    inp = make_inputs(SHAPES["deepseek-v2-lite"], T, device="cpu", hidden=256, inter=128)
+    g = torch.Generator().manual_seed(T)
+    bias = torch.randn(inp.logits.shape[1], generator=g) * 0.1
+    kw = dict(scoring_func="sigmoid", n_group=8, topk_group=4, e_score_correction_bias=bias.to(dev),
+              routed_scaling_factor=2.5)
+    s = inp.shape
+    out, ids, w = ops.fused_moe(inp.x.to(dev), inp.logits.to(dev), s.top_k, inp.w_gate_up.to(dev),
+                                inp.w_down.to(dev), shared_gate_up=inp.shared_gate_up.to(dev),
+                                shared_down=inp.shared_down.to(dev), out_dtype=torch.float32, return_routing=True, **kw)
+    rid, rw = oracle.route_grouped_topk(inp.logits, s.top_k, 8, 4, bias, True, 2.5)
+    assert torch.equal(cpu(ids), rid)
+    torch.testing.assert_close(cpu(w), rw, rtol=2e-6, atol=1e-7)
+    ref = oracle.moe_forward(inp.x.cpu(), inp.logits.cpu(), s.top_k, inp.w_gate_up.cpu(), inp.w_down.cpu(), True,
+                             inp.shared_gate_up.cpu(), inp.shared_down.cpu(), routing=(rid, rw))
+    assert oracle.rel_l2(cpu(out), ref) <= 1e-2
+    # the same routing passed in explicitly (EIMOE_ROUTING_IN) gives the same output bit for bit
+    out2 = ops.fused_moe(inp.x.to(dev), None, s.top_k, inp.w_gate_up.to(dev), inp.w_down.to(dev),
+                         shared_gate_up=inp.shared_gate_up.to(dev), shared_down=inp.shared_down.to(dev),
+                         out_dtype=torch.float32, routing=(ids, w), num_experts=inp.logits.shape[1])
+    assert torch.equal(out, out2)
+
+
 # --------------------------------------------------------------------------- real shapes
 REAL = [("tiny-mixtral-fp32", 512), ("mixtral-8x7b", 64), ("mixtral-8x7b", 8192), ("deepseek-v2-lite", 4096),
         ("qwen3-30b-a3b-local32", 1), ("qwen3-30b-a3b-local32", 32), ("qwen3-30b-a3b-local32", 256),

@@ -260,3 +260,73 @@ def test_grouped_gemm_single_contract():
     out = oracle.grouped_gemm(a, bs, [4, 0, 5])
     torch.testing.assert_close(out[:4], a[:4] @ bs[0].T)
     torch.testing.assert_close(out[4:], a[4:] @ bs[2].T)
+
+
+# --------------------------------------------------------------------------- DeepSeek-V3 gate
+def _v3_gate_literal(logits, k, n_group, topk_group, bias, norm, scaling):
+    """modeling_deepseek_v3.py:151-203 transcribed line by line in torch fp32 (sorted=False
+    top-k calls included): the check for oracle.route_grouped_topk, not the oracle itself."""
+    seq_len = logits.shape[0]
+    E = logits.shape[1]
+    scores = logits.float().sigmoid()
+    scores_for_choice = scores.view(seq_len, -1) + bias.unsqueeze(0)
+    group_scores = scores_for_choice.view(seq_len, n_group, -1).topk(2, dim=-1)[0].sum(dim=-1)
+    group_idx = torch.topk(group_scores, k=topk_group, dim=-1, sorted=False)[1]
+    group_mask = torch.zeros_like(group_scores)
+    group_mask.scatter_(1, group_idx, 1)
+    score_mask = group_mask.unsqueeze(-1).expand(seq_len, n_group, E // n_group).reshape(seq_len, -1)
+    tmp_scores = scores_for_choice.masked_fill(~score_mask.bool(), 0.0)
+    _, topk_idx = torch.topk(tmp_scores, k=k, dim=-1, sorted=False)
+    topk_weight = scores.gather(1, topk_idx)
+    if k > 1 and norm:
+        topk_weight = topk_weight / (topk_weight.sum(dim=-1, keepdim=True) + 1e-20)
+    return topk_idx, topk_weight * scaling
+
+
+@pytest.mark.parametrize("T,E,k,ng,tg,norm,scale", [(300, 256, 8, 8, 4, True, 2.5), (200, 64, 6, 1, 1, True, 2.446),
+                                                    (100, 160, 6, 10, 3, False, 1.0), (50, 512, 32, 256, 16, True, 1.5)])
+def test_grouped_router_matches_reference_lines(T, E, k, ng, tg, norm, scale):
+    g = torch.Generator().manual_seed(E + k)
+    logits = torch.randn(T, E, generator=g) * 2
+    bias = torch.randn(E, generator=g) * 0.1
+    ids, w = oracle.route_grouped_topk(logits, k, ng, tg, bias, norm, scale)
+    rid, rw = _v3_gate_literal(logits, k, ng, tg, bias, norm, scale)
+    # the reference's order is unspecified (sorted=False): compare per token as sets, and the
+    # weights matched by expert id; fp32 sigmoid vs the correctly rounded one is ~1 ulp
+    for t in range(T):
+        a = dict(zip(ids[t].tolist(), w[t].tolist()))
+        b = dict(zip(rid[t].tolist(), rw[t].tolist()))
+        assert set(a) == set(b), t
+        for e in a:
+            assert abs(a[e] - b[e]) <= 2e-6 * max(1.0, abs(b[e])), (t, e)
+
+
+def test_grouped_router_known_answer():
+    # E=8 in 4 groups of 2, keep 2 groups, k=2.  sigmoid(l) ~ [.953 .047 .622 .599 .881 .870 .269 .971];
+    # group top-2 sums ~ [1.000 1.221 1.751 1.240].  Without a bias groups 2 and 3 are kept and
+    # the picks are 7, 4; a -0.9 correction on expert 7 drops group 3 to ~0.34, so groups 2 and
+    # 1 are kept and the picks are 4, 5.  Expert 0 (second largest sigmoid) is never picked:
+    # its group is not kept.
+    logits = torch.tensor([[3.0, -3.0, 0.5, 0.4, 2.0, 1.9, -1.0, 3.5]])
+    s = 1 / (1 + np.exp(-logits.double().numpy()[0]))
+    ids, w = oracle.route_grouped_topk(logits, 2, 4, 2, None, True, 2.0)
+    assert ids.tolist() == [[7, 4]]
+    np.testing.assert_allclose(w.numpy()[0], np.array([s[7], s[4]]) / (s[7] + s[4]) * 2.0, rtol=1e-6)
+    bias = torch.tensor([0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, -0.9])
+    ids, w = oracle.route_grouped_topk(logits, 2, 4, 2, bias, True, 2.0)
+    assert ids.tolist() == [[4, 5]]
+    np.testing.assert_allclose(w.numpy()[0], np.array([s[4], s[5]]) / (s[4] + s[5]) * 2.0, rtol=1e-6)
+    ids, w = oracle.route_grouped_topk(logits, 2, 4, 2, bias, False, 1.0)   # no renormalisation
+    np.testing.assert_allclose(w.numpy()[0], np.array([s[4], s[5]]), rtol=1e-6)
+
+
+def test_grouped_router_masked_experts_score_zero():
+    # Every corrected score inside the kept groups is negative, so the experts masked to 0.0
+    # (masked_fill, not -inf) win, the lowest ids first; weights are their unbiased sigmoids.
+    logits = torch.full((1, 8), -4.0)
+    logits[0, 0] = -3.0
+    bias = torch.full((8,), -0.5)
+    ids, w = oracle.route_grouped_topk(logits, 3, 4, 1, bias, False, 1.0)
+    # group 0 kept (largest top-2 sum); masked groups contribute experts 2, 3, 4 at 0.0
+    assert ids.tolist() == [[2, 3, 4]]
+    np.testing.assert_allclose(w.numpy()[0], 1 / (1 + np.exp(4.0)) * np.ones(3), rtol=1e-6)
