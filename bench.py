@@ -15,6 +15,9 @@ Prints ONE JSON line.  Besides the contract fields it carries:
                 bounded token sample, timed on this host
   layer / decode / kernels_ms   whole-layer TFLOP/s, the 64-token decode batch
                 (HBM-bound) and the per-kernel breakdown
+  suite         the other workloads, warm and cache-cold: tiny fp32, DeepSeek-V2-Lite
+                (zipf + uniform twin, and routed by the DeepSeek-V3 gate), the DeepSeek-V3
+                gate alone, the Qwen3 local share at 1..2048 tokens, fp8 W8A8 Mixtral
 """
 from __future__ import annotations
 
@@ -168,6 +171,20 @@ def traffic_run(torch, ops, shape, make_inputs, tokens):
     print("traffic run done", flush=True)
 
 
+def settle(fn, warmup, torch, min_s=0.05):
+    """Run a suite case until at least ``min_s`` seconds of it have executed (and ``warmup``
+    calls): a freshly drawn workload measured ~10 % slow over its first few milliseconds
+    (DeepSeek-V2-Lite zipf, 0.85 ms on the first timing vs 0.77 ms on later ones)."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < min_s:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def timed_cold(fn, steps, warmup, torch, flush):
     """Mean ms of fn with the device caches flushed before every call (each call bracketed by
     HIP events on the launch stream, the flush outside them): weights of a small layer would
@@ -186,7 +203,7 @@ def timed_cold(fn, steps, warmup, torch, flush):
     return sum(a.elapsed_time(b) for a, b in evs) / steps
 
 
-def layer_case(name, inp, torch, ops, steps, warmup, flush, *, w8a8=False, fp8w=None):
+def layer_case(name, inp, torch, ops, steps, warmup, flush, *, w8a8=False, fp8w=None, router_kw=None):
     """One fused-layer workload: warm and cache-cold times, tokens/s, TFLOP/s and HBM GB/s."""
     from easyinfra_amd.workloads import layer_flops, layer_bytes
     s = inp.shape
@@ -198,7 +215,7 @@ def layer_case(name, inp, torch, ops, steps, warmup, flush, *, w8a8=False, fp8w=
         wgu, wd, scales = fp8w
     Is = inp.shared_down.shape[1] if inp.shared_down is not None else 0
     kw = dict(renormalize=s.renormalize, shared_gate_up=inp.shared_gate_up, shared_down=inp.shared_down,
-              expert_range=inp.expert_range, w_scales=scales, w8a8=w8a8)
+              expert_range=inp.expert_range, w_scales=scales, w8a8=w8a8, **(router_kw or {}))
     ws = torch.empty(ops.fused_moe_workspace_bytes(T, H, I, s.n_experts, s.top_k, n_local, Is,
                                                    flags=4 if w8a8 else 0), dtype=torch.uint8, device=inp.x.device)
     fn = lambda: ops.fused_moe(inp.x, inp.logits, s.top_k, wgu, wd, workspace=ws, **kw)
@@ -207,6 +224,7 @@ def layer_case(name, inp, torch, ops, steps, warmup, flush, *, w8a8=False, fp8w=
     local = ids[(ids >= lo) & (ids < hi)]
     A = int(local.numel())
     touched = int(torch.unique(local).numel())
+    settle(fn, warmup, torch)
     ms = timed(fn, steps, warmup, torch)
     ms_cold = timed_cold(fn, steps, 1, torch, flush)
     flops = layer_flops(A, T, H, I, Is)
@@ -216,6 +234,24 @@ def layer_case(name, inp, torch, ops, steps, warmup, flush, *, w8a8=False, fp8w=
     return {"case": name, "tokens": T, "assignments": A, "touched_experts": touched, "ms": round(ms, 4),
             "ms_cold": round(ms_cold, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
             "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / peak, 4),
+            "hbm_GBps_cold": round(nbytes / (ms_cold * 1e-3) / 1e9, 1),
+            "hbm_frac_cold": round(nbytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def gate_case(torch, ops, steps, warmup, flush):
+    """The DeepSeek-V3 gate alone: 4096 tokens x 256 experts, 8 groups keep 4, top-8 (HBM-bound:
+    logits in, ids and weights out)."""
+    T, E, k = 4096, 256, 8
+    g = torch.Generator(device="cuda").manual_seed(5)
+    logits = torch.randn(T, E, device="cuda", generator=g) * 2
+    bias = torch.randn(E, device="cuda", generator=g) * 0.1
+    fn = lambda: ops.router_grouped_topk(logits, k, 8, 4, bias, True, 2.5)
+    settle(fn, warmup, torch)
+    ms = timed(fn, steps, warmup, torch)
+    ms_cold = timed_cold(fn, steps, 1, torch, flush)
+    nbytes = T * E * 4 + E * 4 + T * k * 8
+    return {"case": f"DeepSeek-V3 gate alone T={T} E={E} k={k} (8 groups keep 4)", "tokens": T, "ms": round(ms, 4),
+            "ms_cold": round(ms_cold, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
             "hbm_GBps_cold": round(nbytes / (ms_cold * 1e-3) / 1e9, 1),
             "hbm_frac_cold": round(nbytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
@@ -237,6 +273,16 @@ def suite(torch, ops, mix_inp, steps, warmup):
                      torch, ops, steps, warmup, flush)
     skew["skew_over_uniform"] = round(skew["ms"] / uni["ms"], 3)
     out += [skew, uni]
+    # the DeepSeek-V3 gate (sigmoid, correction bias, 8 groups keep 4, scaling 2.5) routing the
+    # same layer, and the gate alone at DeepSeek-V3's own size (4096 tokens, 256 experts, top-8)
+    ds_inp = make_inputs(ds, 4096, device=dev)
+    bias = torch.randn(ds.n_experts, device=dev, generator=torch.Generator(device=dev).manual_seed(3)) * 0.1
+    v3 = dict(scoring_func="sigmoid", n_group=8, topk_group=4, e_score_correction_bias=bias,
+              routed_scaling_factor=2.5)
+    out.append(layer_case("deepseek-v2-lite T=4096 + 2 shared, DeepSeek-V3 gate (8 groups keep 4)", ds_inp, torch,
+                          ops, steps, warmup, flush, router_kw=v3))
+    del ds_inp
+    out.append(gate_case(torch, ops, steps, warmup, flush))
     qw = SHAPES["qwen3-30b-a3b-local32"]
     for T in (1, 32, 256, 2048):
         hot = layer_case(f"qwen3-30b-a3b local 32/128 T={T} hot:cold 8:1", make_inputs(qw, T, device=dev), torch, ops,
