@@ -312,6 +312,22 @@ int eimoe_router_grouped_topk(const float* logits, int T, int E, int k, int n_gr
                    "router_grouped_topk");
 }
 
+int eimoe_eplb_map(const int32_t* topk_ids, int T, int k, const int32_t* log2phy, int n_logical, int max_replicas,
+                   const int32_t* replica_count, int32_t* physical_ids, void* stream) {
+  if (T < 0 || k < 1) return fail(EIMOE_ERR_SHAPE, "T=%d, k=%d", T, k);
+  if (static_cast<long long>(T) * k > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "T*k overflows int32");
+  if (n_logical < 1 || max_replicas < 1 || static_cast<long long>(n_logical) * max_replicas > 0x7fffffffll)
+    return fail(EIMOE_ERR_SHAPE, "n_logical=%d, max_replicas=%d", n_logical, max_replicas);
+  if (T == 0) return EIMOE_OK;
+  REQUIRE_PTR(topk_ids);
+  REQUIRE_PTR(log2phy);
+  REQUIRE_PTR(replica_count);
+  REQUIRE_PTR(physical_ids);
+  return hip_check(launch_eplb_map(topk_ids, T * k, log2phy, n_logical, max_replicas, replica_count, physical_ids,
+                                   S(stream)),
+                   "eplb_map");
+}
+
 int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, int32_t* counts, int32_t* offsets,
                 int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream) {
   if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);

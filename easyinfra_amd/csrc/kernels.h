@@ -46,6 +46,9 @@ hipError_t launch_router_topk(const float* logits, int T, int E, int k, int reno
 hipError_t launch_router_grouped(const float* logits, int T, int E, int k, int n_group, int topk_group,
                                  const float* bias, int renorm, float scaling, int32_t* ids, float* w,
                                  hipStream_t s);
+// EPLB logical -> physical ids (replica i mod count of each flat slot i); in place allowed.
+hipError_t launch_eplb_map(const int32_t* ids, int n, const int32_t* log2phy, int n_logical, int max_rep,
+                           const int32_t* replica_count, int32_t* phys, hipStream_t s);
 size_t align_lds_bytes(int n_loc);
 hipError_t launch_align(const int32_t* ids, int T, int k, int e_lo, int n_loc, int32_t* counts, int32_t* offsets,
                         int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, hipStream_t s);

@@ -215,6 +215,36 @@ hipError_t launch_router_grouped(const float* logits, int T, int E, int k, int n
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------- EPLB
+// Logical -> physical expert ids (eplb_map_to_physical_and_record, generation/blocks/moe/
+// base.py:40-64): slot i of the flattened [T,k] ids takes replica i mod count[id] of its
+// logical expert, so repeated picks of one expert spread over its replicas
+// deterministically.  Ids outside [0, n_logical) (or a count outside [1, max_rep]) map to -1.
+__global__ __launch_bounds__(256) void eplb_map_kernel(const int32_t* __restrict__ ids, int n,
+                                                       const int32_t* __restrict__ log2phy, int n_logical,
+                                                       int max_rep, const int32_t* __restrict__ replica_count,
+                                                       int32_t* __restrict__ phys) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    const int l = ids[i];
+    int out = -1;
+    if (l >= 0 && l < n_logical) {
+      const int c = replica_count[l];
+      if (c >= 1 && c <= max_rep) out = log2phy[static_cast<long long>(l) * max_rep + i % c];
+    }
+    phys[i] = out;
+  }
+}
+
+hipError_t launch_eplb_map(const int32_t* ids, int n, const int32_t* log2phy, int n_logical, int max_rep,
+                           const int32_t* replica_count, int32_t* phys, hipStream_t s) {
+  int blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(eplb_map_kernel, dim3(blocks), dim3(256), 0, s, ids, n, log2phy, n_logical, max_rep,
+                     replica_count, phys);
+  return hipGetLastError();
+}
+
 // Router and align in one workgroup, for batches its 16 waves route in a few steps: the
 // ids stay in LDS between the two phases, and one launch (a few microseconds of dispatch
 // and cold-cache latency at decode sizes) replaces two.  Same outputs as the two kernels.

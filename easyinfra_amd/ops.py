@@ -72,6 +72,40 @@ def router_grouped_topk(logits: torch.Tensor, top_k: int, n_group: int = 1, topk
     return ids, w
 
 
+def eplb_default_layout(num_logical: int, ep_size: int, num_physical: int):
+    """The default replica layout of _MoeBlock (generation/blocks/moe/base.py:162-185), built on
+    the host: each of ``ep_size`` ranks holds ``num_physical`` physical experts, its share of
+    the logical experts followed by replicas of the next ones.  Returns (phy2log [ep, P],
+    log2phy [L, max_replicas] (-1 padded), replica_count [L]), int32 CPU tensors."""
+    base_n = num_logical // ep_size
+    if base_n * ep_size != num_logical or num_physical < base_n:
+        raise ValueError(f"{num_logical} logical experts over ep={ep_size} with {num_physical} physical per rank")
+    base = torch.arange(base_n * ep_size).view(ep_size, base_n)
+    tail = torch.arange(1, num_physical - base_n + 1)[None, :] + base[:, -1:]
+    phy2log = torch.cat([base, tail], dim=-1) % num_logical
+    flat = phy2log.reshape(-1)
+    count = torch.bincount(flat, minlength=num_logical)
+    log2phy = torch.full((num_logical, int(count.max())), -1, dtype=torch.long)
+    fill = torch.zeros(num_logical, dtype=torch.long)
+    for p, l in enumerate(flat.tolist()):
+        log2phy[l, fill[l]] = p
+        fill[l] += 1
+    return phy2log.to(torch.int32), log2phy.to(torch.int32), count.to(torch.int32)
+
+
+def eplb_map(topk_ids: torch.Tensor, log2phy: torch.Tensor, replica_count: torch.Tensor,
+             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Logical -> physical expert ids (base.py:40-64): replica (t*k + slot) mod count."""
+    _req(topk_ids, "topk_ids", torch.int32, 2)
+    _req(log2phy, "log2phy", torch.int32, 2)
+    _req(replica_count, "replica_count", torch.int32, 1)
+    T, k = topk_ids.shape
+    out = torch.empty_like(topk_ids) if out is None else out
+    call("eimoe_eplb_map", topk_ids.data_ptr(), T, k, log2phy.data_ptr(), log2phy.shape[0], log2phy.shape[1],
+         replica_count.data_ptr(), out.data_ptr(), _stream(topk_ids))
+    return out
+
+
 def align(topk_ids: torch.Tensor, n_local: int, e_lo: int = 0) -> dict:
     """Counts/offsets/stable permutation (blocks/moe/base.py:343-364, moe_all2all.py:346-348)."""
     _req(topk_ids, "topk_ids", torch.int32, 2)

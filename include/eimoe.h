@@ -85,6 +85,15 @@ int eimoe_router_grouped_topk(const float* logits, int T, int E, int k, int n_gr
                               const float* bias, int renormalize, float scaling, int32_t* topk_ids,
                               float* topk_weights, void* stream);
 
+/* EPLB logical -> physical expert ids: eplb_map_to_physical_and_record
+ * (generation/blocks/moe/base.py:40-64), with the maps built at base.py:162-185.
+ * physical_ids[i] = log2phy[topk_ids[i]][i % replica_count[topk_ids[i]]] over the flattened
+ * [T,k] ids (i = t*k + slot), so repeated picks of one logical expert spread over its replicas.
+ * log2phy [n_logical, max_replicas] int32, replica_count [n_logical] int32.  Ids outside
+ * [0, n_logical) map to -1.  physical_ids may alias topk_ids. */
+int eimoe_eplb_map(const int32_t* topk_ids, int T, int k, const int32_t* log2phy, int n_logical, int max_replicas,
+                   const int32_t* replica_count, int32_t* physical_ids, void* stream);
+
 /* Align: per-expert counts, offsets and the stable expert-major permutation.
  * Replaces _MoeBlock._all_expert_count_compute (generation/blocks/moe/base.py:343-364) and the
  * sort/index steps of MoeAll2AllBlock.all2all_chunk_routing_compute (blocks/moe/moe_all2all.py:346-348).

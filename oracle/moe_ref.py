@@ -13,6 +13,7 @@ with every collective replaced by the identity it is at group size 1
   route_topk     modeling_qwen3_moe.py:255-266 (softmax -> top-k -> renorm)
   route_grouped_topk  modeling_deepseek_v3.py:151-203 (DeepSeek-V3 gate: sigmoid,
                  correction bias, group-limited top-k, renorm, scaling)
+  eplb_map       blocks/moe/base.py:40-64 (EPLB logical -> physical replica ids)
   align          blocks/moe/base.py:343-364 (per-expert counts),
                  moe_all2all.py:346-348 (sort, token index, slot), with the
                  EP-local expert window of blocks/moe/base.py:162-169, 187
@@ -122,6 +123,21 @@ def route_grouped_topk(logits, k: int, n_group: int, topk_group: int, bias=None,
         w = (w / (w.sum(axis=-1, keepdims=True, dtype=np.float32) + np.float32(1e-20))).astype(np.float32)
     w = (w * np.float32(scaling)).astype(np.float32)
     return torch.from_numpy(ids.astype(np.int32)), torch.from_numpy(w)
+
+
+def eplb_map(ids, log2phy, replica_count) -> torch.Tensor:
+    """eplb_map_to_physical_and_record (generation/blocks/moe/base.py:40-64): flat slot i of
+    the [T,k] ids takes replica i % replica_count[id] of its logical expert.  Ids outside
+    [0, L) map to -1 (the reference would index out of range)."""
+    ids = np.asarray(torch.as_tensor(ids)).astype(np.int64)
+    l2p = np.asarray(torch.as_tensor(log2phy)).astype(np.int64)
+    cnt = np.asarray(torch.as_tensor(replica_count)).astype(np.int64)
+    flat = ids.reshape(-1)
+    out = np.full(flat.shape, -1, np.int64)
+    for i, l in enumerate(flat):
+        if 0 <= l < l2p.shape[0] and 1 <= cnt[l] <= l2p.shape[1]:
+            out[i] = l2p[l, i % cnt[l]]
+    return torch.from_numpy(out.reshape(ids.shape).astype(np.int32))
 
 
 # --------------------------------------------------------------------------- align

@@ -76,6 +76,14 @@ def test_router_grouped_validation():
     assert _rc(f, None, 0, 256, 8, 8, 4, None, 1, 1.0, None, None, None) == _lib.EIMOE_OK
 
 
+def test_eplb_map_validation():
+    f = "eimoe_eplb_map"
+    assert _rc(f, None, 4, 0, None, 8, 2, None, None, None) == _lib.ERR_SHAPE    # k = 0
+    assert _rc(f, None, 4, 2, None, 0, 2, None, None, None) == _lib.ERR_SHAPE    # no logical experts
+    assert _rc(f, None, 4, 2, None, 8, 2, None, None, None) == _lib.ERR_NULL
+    assert _rc(f, None, 0, 2, None, 8, 2, None, None, None) == _lib.EIMOE_OK
+
+
 def test_gemm_validation():
     # H not a multiple of 64
     assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 100, 1, _lib.BF16, None, 100, 64, 1, 1, 1, 4, 1, 0,

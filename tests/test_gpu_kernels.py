@@ -90,6 +90,22 @@ def test_router_grouped_empty(dev):
     assert ids.shape == (0, 6)
 
 
+# --------------------------------------------------------------------------- EPLB replica map
+@pytest.mark.parametrize("L,ep,P,T,k", [(8, 2, 5, 3, 2), (64, 4, 20, 500, 6), (256, 8, 40, 1000, 8), (128, 1, 128, 7, 8)])
+def test_eplb_map_matches_oracle(dev, L, ep, P, T, k):
+    _, log2phy, count = ops.eplb_default_layout(L, ep, P)
+    g = torch.Generator().manual_seed(L + T)
+    ids = torch.randint(0, L, (T, k), generator=g, dtype=torch.int32)
+    ids[0, 0] = -1                                   # out of range -> -1
+    ids[-1, -1] = L
+    want = oracle.eplb_map(ids, log2phy, count)
+    got = ops.eplb_map(ids.to(dev), log2phy.to(dev), count.to(dev))
+    assert torch.equal(cpu(got), want)
+    inplace = ids.to(dev)
+    ops.eplb_map(inplace, log2phy.to(dev), count.to(dev), out=inplace)
+    assert torch.equal(cpu(inplace), want)
+
+
 # --------------------------------------------------------------------------- align
 @pytest.mark.parametrize("T,k,E,e_lo,n_loc,skew", [
     (1, 2, 8, 0, 8, False), (512, 2, 8, 0, 8, False), (8192, 2, 8, 0, 8, False), (4096, 6, 64, 0, 64, True),

@@ -117,6 +117,28 @@ def test_layer_deepseek_v3_gate(dev, T):
     assert torch.equal(out, out2)
 
 
+def test_layer_with_eplb_replicas_matches_logical_layer(dev):
+    """Physical experts are copies of logical ones, so routing through the EPLB map (replica
+    i mod count of each flat slot) onto physically laid-out weights reproduces the logical
+    layer: router -> eplb_map -> fused layer with EIMOE_ROUTING_IN."""
+    inp = make_inputs(SHAPES["qwen3-30b-a3b-local32"], 64, device="cpu", hidden=256, inter=128)
+    s = inp.shape
+    E = inp.logits.shape[1]
+    wgu_log = torch.randn(E, 2 * 128, 256, generator=torch.Generator().manual_seed(1)) * 0.05
+    wd_log = torch.randn(E, 256, 128, generator=torch.Generator().manual_seed(2)) * 0.05
+    wgu_log, wd_log = wgu_log.to(torch.bfloat16).to(dev), wd_log.to(torch.bfloat16).to(dev)
+    phy2log, log2phy, count = ops.eplb_default_layout(E, 4, E // 4 + 8)   # 8 replicas per rank
+    flat = phy2log.reshape(-1).long().to(dev)
+    x, lg = inp.x.to(dev), inp.logits.to(dev)
+    ids, w = ops.router_topk(lg, s.top_k, s.renormalize)
+    phys = ops.eplb_map(ids, log2phy.to(dev), count.to(dev))
+    assert torch.equal(flat[phys.long()], ids.long())
+    logical = ops.fused_moe(x, lg, s.top_k, wgu_log, wd_log, renormalize=s.renormalize, out_dtype=torch.float32)
+    physical = ops.fused_moe(x, None, s.top_k, wgu_log[flat], wd_log[flat], out_dtype=torch.float32,
+                             routing=(phys, w), num_experts=flat.numel())
+    assert oracle.rel_l2(cpu(physical), cpu(logical)) <= 1e-5
+
+
 # --------------------------------------------------------------------------- real shapes
 REAL = [("tiny-mixtral-fp32", 512), ("mixtral-8x7b", 64), ("mixtral-8x7b", 8192), ("deepseek-v2-lite", 4096),
         ("qwen3-30b-a3b-local32", 1), ("qwen3-30b-a3b-local32", 32), ("qwen3-30b-a3b-local32", 256),

@@ -330,3 +330,37 @@ def test_grouped_router_masked_experts_score_zero():
     # group 0 kept (largest top-2 sum); masked groups contribute experts 2, 3, 4 at 0.0
     assert ids.tolist() == [[2, 3, 4]]
     np.testing.assert_allclose(w.numpy()[0], 1 / (1 + np.exp(4.0)) * np.ones(3), rtol=1e-6)
+
+
+# --------------------------------------------------------------------------- EPLB replica map
+def test_eplb_default_layout_and_map_known_answer():
+    from easyinfra_amd.ops import eplb_default_layout
+    # 8 logical experts over 2 ranks of 5 physical slots (base.py:162-185): rank r holds its 4
+    # experts and replicates the next one (mod 8): physical 0..4 -> 0 1 2 3 4, 5..9 -> 4 5 6 7 0
+    phy2log, log2phy, count = eplb_default_layout(8, 2, 5)
+    assert phy2log.tolist() == [[0, 1, 2, 3, 4], [4, 5, 6, 7, 0]]
+    assert count.tolist() == [2, 1, 1, 1, 2, 1, 1, 1]
+    assert log2phy[0].tolist() == [0, 9] and log2phy[4].tolist() == [4, 5] and log2phy[5].tolist() == [6, -1]
+    # flat slot i takes replica i % count: expert 0 at slots 0, 2 -> replica 0 (physical 0),
+    # expert 4 at slots 1, 3 -> replica 1 (physical 5); swapped columns flip the replicas
+    ids = torch.tensor([[0, 4], [0, 4]], dtype=torch.int32)
+    assert oracle.eplb_map(ids, log2phy, count).tolist() == [[0, 5], [0, 5]]
+    ids = torch.tensor([[4, 0], [4, 0], [1, 7]], dtype=torch.int32)
+    assert oracle.eplb_map(ids, log2phy, count).tolist() == [[4, 9], [4, 9], [1, 8]]
+    assert oracle.eplb_map(torch.tensor([[-1, 8]], dtype=torch.int32), log2phy, count).tolist() == [[-1, -1]]
+
+
+def test_eplb_map_invariants():
+    from easyinfra_amd.ops import eplb_default_layout
+    phy2log, log2phy, count = eplb_default_layout(64, 4, 20)
+    g = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, 64, (500, 6), generator=g, dtype=torch.int32)
+    phys = oracle.eplb_map(ids, log2phy, count)
+    flat_p2l = phy2log.reshape(-1)
+    assert torch.equal(flat_p2l[phys.long()], ids)                     # every pick keeps its logical expert
+    # a replicated expert's picks alternate over its replicas with the flat slot parity
+    for l in torch.nonzero(count > 1).flatten().tolist():
+        sel = (ids.reshape(-1) == l).nonzero().flatten()
+        got = phys.reshape(-1)[sel]
+        want = log2phy[l][(sel % int(count[l])).long()]
+        assert torch.equal(got, want)
