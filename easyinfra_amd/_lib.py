@@ -15,6 +15,7 @@ EIMOE_OK = 0
 ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_WORKSPACE, ERR_HIP = -1, -2, -3, -4, -5, -6
 F32, BF16, FP8 = 0, 1, 2
 RENORMALIZE, Y_F32, W8A8, ROUTING_IN = 1, 2, 4, 8
+LOGITS_BF16 = 1   # eimoe_moe_prologue flag
 TILE_AUTO, TILE_256x256, TILE_128x128, TILE_32x128, TILE_16x64, TILE_STREAM = 0, 1, 2, 3, 4, 5
 MAX_TOPK, MAX_EXPERTS, MAX_SEGMENTS = 32, 512, 1024
 
@@ -29,6 +30,9 @@ SIGNATURES = {
     "eimoe_router_grouped_topk": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int, c_float,
                                           c_void_p, c_void_p, c_void_p]),
     "eimoe_eplb_map": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "eimoe_moe_prologue_workspace_bytes": (c_size_t, []),
+    "eimoe_moe_prologue": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_int, c_int, c_int, c_int,
+                                   c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "eimoe_align": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                             c_void_p, c_void_p]),
     "eimoe_route_align": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,

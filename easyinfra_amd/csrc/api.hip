@@ -582,6 +582,40 @@ int eimoe_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, 
   return hip_check(launch_quantize_rows_fp8(x, dtype, rows, cols, q, scale, S(stream)), "quantize_rows_fp8");
 }
 
+size_t eimoe_moe_prologue_workspace_bytes(void) { return 256; }
+
+int eimoe_moe_prologue(const void* hidden, const void* residual, const void* norm_w, float eps, const void* gate_w,
+                       int T, int H, int E, int flags, void* residual_out, void* normed, float* logits,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
+  if (H < 64 || H > 8192 || H % 64) return fail(EIMOE_ERR_ALIGN, "H=%d must be a multiple of 64 in [64, 8192]", H);
+  if (E < 1 || E > EIMOE_MAX_EXPERTS) return fail(EIMOE_ERR_SHAPE, "E=%d outside [1,%d]", E, EIMOE_MAX_EXPERTS);
+  const bool fused = prologue_fused_router(H, E);
+  if (!fused && E % 64)
+    return fail(EIMOE_ERR_SHAPE, "E=%d: up to %d experts with %lld bytes of gate weights, or a multiple of 64", E,
+                kPrologueFusedMaxE, kPrologueFusedMaxGate);
+  if (!(eps >= 0.f)) return fail(EIMOE_ERR_SHAPE, "eps must be >= 0");
+  if (T == 0) return EIMOE_OK;
+  REQUIRE_PTR(hidden);
+  REQUIRE_PTR(residual);
+  REQUIRE_PTR(norm_w);
+  REQUIRE_PTR(gate_w);
+  REQUIRE_PTR(residual_out);
+  REQUIRE_PTR(normed);
+  REQUIRE_PTR(logits);
+  if (normed == residual_out || normed == residual || normed == hidden)
+    return fail(EIMOE_ERR_SHAPE, "normed must not alias the residual or hidden rows");
+  if (!fused) {
+    REQUIRE_PTR(workspace);
+    if (workspace_bytes < eimoe_moe_prologue_workspace_bytes())
+      return fail(EIMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes,
+                  eimoe_moe_prologue_workspace_bytes());
+  }
+  return hip_check(launch_moe_prologue(hidden, residual, norm_w, eps, gate_w, T, H, E, (flags & EIMOE_LOGITS_BF16) ? 1 : 0,
+                                       residual_out, normed, logits, static_cast<int32_t*>(workspace), S(stream)),
+                   "moe_prologue");
+}
+
 size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_local, int shared_inter,
                                        int out_dtype, int flags) {
   (void)E;

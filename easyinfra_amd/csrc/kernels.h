@@ -59,6 +59,17 @@ hipError_t launch_route_align(const float* logits, int T, int E, int k, int reno
                               int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
                               int32_t* sorted_tok, int32_t* pos, hipStream_t s);
 hipError_t launch_counts_to_offsets(const int32_t* counts, int S, int32_t* offsets, hipStream_t s);
+// MoE prologue: residual add + RMSNorm (+ router logits).  Routers of at most
+// kPrologueFusedMaxE experts and kPrologueFusedMaxGate bytes of gate weights are dotted in
+// the same pass; others (E % 64 == 0) go through the grouped GEMM with seg_off[2] as the
+// one dense segment.
+constexpr int kPrologueFusedMaxE = 32;
+constexpr long long kPrologueFusedMaxGate = 128 * 1024;
+bool prologue_fused_router(int H, int E);
+hipError_t launch_moe_prologue(const void* hidden, const void* residual, const void* norm_w, float eps,
+                               const void* gate_w, int T, int H, int E, int logits_bf16, void* res_out, void* normed,
+                               float* logits, int32_t* seg_off, hipStream_t s);
+
 hipError_t launch_gather_rows(const void* x, int row_bytes, const int32_t* rows, const int32_t* num_rows,
                               int max_rows, void* xs, hipStream_t s);
 hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,

@@ -54,6 +54,35 @@ def router_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True) -> T
     return ids, w
 
 
+def moe_prologue(hidden: torch.Tensor, residual: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                 gate_w: torch.Tensor, logits_bf16: bool = True, residual_out: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Residual add, post-attention RMSNorm and router logits in one pass
+    (moe_all2all.py:329-336, base_rmsnorm.py:6-12, base_linear.py:28-36)
+    -> (residual_out [T,H] bf16, normed [T,H] bf16, logits [T,E] fp32).  ``logits_bf16`` rounds the
+    logits to bf16 values (a bf16 gate F.linear: Qwen3, Mixtral); False keeps fp32 (DeepSeek-V3)."""
+    _req(hidden, "hidden", torch.bfloat16, 2)
+    _req(residual, "residual", torch.bfloat16, 2)
+    _req(norm_w, "norm_w", torch.bfloat16, 1)
+    _req(gate_w, "gate_w", torch.bfloat16, 2)
+    T, H = hidden.shape
+    E = gate_w.shape[0]
+    if tuple(residual.shape) != (T, H) or norm_w.numel() != H or gate_w.shape[1] != H:
+        raise ValueError(f"shapes: hidden {tuple(hidden.shape)}, residual {tuple(residual.shape)}, "
+                         f"norm_w {tuple(norm_w.shape)}, gate_w {tuple(gate_w.shape)}")
+    dev = hidden.device
+    res_out = torch.empty_like(residual) if residual_out is None else residual_out
+    normed = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    need = int(_lib.lib().eimoe_moe_prologue_workspace_bytes())
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    call("eimoe_moe_prologue", hidden.data_ptr(), residual.data_ptr(), norm_w.data_ptr(), float(eps),
+         gate_w.data_ptr(), T, H, E, _lib.LOGITS_BF16 if logits_bf16 else 0, res_out.data_ptr(), normed.data_ptr(),
+         logits.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream(hidden))
+    return res_out, normed, logits
+
+
 def router_grouped_topk(logits: torch.Tensor, top_k: int, n_group: int = 1, topk_group: int = 1,
                         bias: Optional[torch.Tensor] = None, renormalize: bool = True,
                         scaling: float = 1.0) -> Tuple[torch.Tensor, torch.Tensor]:

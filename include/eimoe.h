@@ -184,6 +184,26 @@ int eimoe_combine(const void* y, int y_dtype, int n_split, long long split_strid
 int eimoe_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,
                             void* stream);
 
+/* MoE block prologue, one pass over a chunk of hidden states:
+ *   residual_out = residual + hidden                        (bf16; _add_to_residual,
+ *                                                            generation/utils/compute_utils.py:14)
+ *   normed = norm_w * bf16(r * rsqrt(mean(r^2) + eps))       (bf16, r = residual_out in fp32;
+ *                                                            _rmsnorm, modules/norms/base_rmsnorm.py:6-12)
+ *   logits = normed . gate_w^T                               (fp32 accumulation; the router gate)
+ * in the order of MoeAll2AllBlock.all2all_chunk_routing_compute (blocks/moe/moe_all2all.py:329-336).
+ * EIMOE_LOGITS_BF16 rounds the logits to bf16 values (the Qwen3 / Mixtral gate is an F.linear
+ * in bf16, modules/linears/base_linear.py:28-36); without it they stay fp32 (DeepseekV3MoEGate,
+ * models/deepseek_v3/modeling_deepseek_v3.py:155-157).
+ *   hidden, residual, residual_out, normed [T,H] bf16; norm_w [H] bf16; gate_w [E,H] bf16;
+ *   logits [T,E] fp32.  64 <= H <= 8192, H % 64 == 0; E <= 32 with E*H*2 <= 128 KiB (one pass),
+ *   or E % 64 == 0 up to EIMOE_MAX_EXPERTS (router GEMM on the MFMA, needs the workspace).
+ *   residual_out may alias residual; normed may not alias residual_out. */
+enum { EIMOE_LOGITS_BF16 = 1 };
+size_t eimoe_moe_prologue_workspace_bytes(void);
+int eimoe_moe_prologue(const void* hidden, const void* residual, const void* norm_w, float eps, const void* gate_w,
+                       int T, int H, int E, int flags, void* residual_out, void* normed, float* logits,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes for eimoe_fused_moe with these sizes and flags. */
 size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_local, int shared_inter,
                                        int out_dtype, int flags);

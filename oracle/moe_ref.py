@@ -14,6 +14,8 @@ with every collective replaced by the identity it is at group size 1
   route_grouped_topk  modeling_deepseek_v3.py:151-203 (DeepSeek-V3 gate: sigmoid,
                  correction bias, group-limited top-k, renorm, scaling)
   eplb_map       blocks/moe/base.py:40-64 (EPLB logical -> physical replica ids)
+  moe_prologue   moe_all2all.py:329-336 (residual add), base_rmsnorm.py:6-12 (RMSNorm),
+                 base_linear.py:28-36 / modeling_deepseek_v3.py:155-157 (router logits)
   align          blocks/moe/base.py:343-364 (per-expert counts),
                  moe_all2all.py:346-348 (sort, token index, slot), with the
                  EP-local expert window of blocks/moe/base.py:162-169, 187
@@ -138,6 +140,32 @@ def eplb_map(ids, log2phy, replica_count) -> torch.Tensor:
         if 0 <= l < l2p.shape[0] and 1 <= cnt[l] <= l2p.shape[1]:
             out[i] = l2p[l, i % cnt[l]]
     return torch.from_numpy(out.reshape(ids.shape).astype(np.int32))
+
+
+def moe_prologue(hidden, residual, norm_w, eps: float, gate_w, logits_bf16: bool = True):
+    """The MoE block's prologue: MoeAll2AllBlock.all2all_chunk_routing_compute
+    (generation/blocks/moe/moe_all2all.py:329-336):
+      residual = residual + hidden                           (compute_utils.py:14, bf16)
+      normed = _rmsnorm(residual, weight, eps)               (base_rmsnorm.py:6-12):
+               t = r.float(); t = t * rsqrt(mean(t^2) + eps); weight * t.to(bf16)
+      logits = F.linear(normed, gate_w)                      (base_linear.py:28-36, bf16: Qwen3,
+               Mixtral)  or  F.linear(normed.float(), gate_w.float())  (DeepseekV3MoEGate,
+               modeling_deepseek_v3.py:155-157)
+    bf16 tensors in, (residual [T,H] bf16, normed [T,H] bf16, logits [T,E] fp32) out."""
+    hidden = torch.as_tensor(hidden).to(torch.bfloat16)
+    residual = torch.as_tensor(residual).to(torch.bfloat16)
+    norm_w = torch.as_tensor(norm_w).to(torch.bfloat16)
+    gate_w = torch.as_tensor(gate_w).to(torch.bfloat16)
+    r = residual + hidden
+    t = r.to(torch.float32)
+    variance = t.pow(2).mean(-1, keepdim=True)
+    t = t * torch.rsqrt(variance + eps)
+    normed = norm_w * t.to(torch.bfloat16)
+    if logits_bf16:
+        logits = F.linear(normed, gate_w).float()
+    else:
+        logits = F.linear(normed.float(), gate_w.float())
+    return r, normed, logits
 
 
 # --------------------------------------------------------------------------- align

@@ -84,6 +84,16 @@ def test_eplb_map_validation():
     assert _rc(f, None, 0, 2, None, 8, 2, None, None, None) == _lib.EIMOE_OK
 
 
+def test_moe_prologue_validation():
+    f = "eimoe_moe_prologue"
+    n = [None] * 3
+    assert _rc(f, None, None, None, 1e-6, None, 4, 100, 8, 0, *n, None, 0, None) == _lib.ERR_ALIGN    # H % 64
+    assert _rc(f, None, None, None, 1e-6, None, 4, 16384, 8, 0, *n, None, 0, None) == _lib.ERR_ALIGN  # H > 8192
+    assert _rc(f, None, None, None, 1e-6, None, 4, 4096, 48, 0, *n, None, 0, None) == _lib.ERR_SHAPE  # 48 experts
+    assert _rc(f, None, None, None, 1e-6, None, 4, 4096, 8, 0, *n, None, 0, None) == _lib.ERR_NULL
+    assert _rc(f, None, None, None, 1e-6, None, 0, 4096, 8, 0, *n, None, 0, None) == _lib.EIMOE_OK
+
+
 def test_gemm_validation():
     # H not a multiple of 64
     assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 100, 1, _lib.BF16, None, 100, 64, 1, 1, 1, 4, 1, 0,

@@ -106,6 +106,51 @@ def test_eplb_map_matches_oracle(dev, L, ep, P, T, k):
     assert torch.equal(cpu(inplace), want)
 
 
+# --------------------------------------------------------------------------- MoE prologue
+# One pass for small routers (gate staged in LDS; the 8 x 7168 gate is 114 KiB), the MFMA
+# router GEMM for E a multiple of 64 (Qwen3 128, DeepSeek-V3 256).
+@pytest.mark.parametrize("T,H,E,lbf16", [(1, 4096, 8, True), (300, 4096, 8, True), (257, 2048, 16, True),
+                                         (64, 7168, 8, False), (33, 64, 32, True), (100, 2048, 128, True),
+                                         (257, 7168, 256, False), (1, 4096, 64, True)])
+def test_moe_prologue_matches_oracle(dev, T, H, E, lbf16):
+    g = torch.Generator().manual_seed(T + H + E)
+    hid = (torch.randn(T, H, generator=g) * 2).to(torch.bfloat16)
+    res = (torch.randn(T, H, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    gw = (0.05 * torch.randn(E, H, generator=g)).to(torch.bfloat16)
+    r, normed, logits = ops.moe_prologue(hid.to(dev), res.to(dev), w.to(dev), 1e-6, gw.to(dev), lbf16)
+    rr, rn, rl = oracle.moe_prologue(hid, res, w, 1e-6, gw, lbf16)
+    assert torch.equal(cpu(r), rr)                                   # the bf16 add is exact
+    # the fp32 mean of squares sums in another order: bf16(r * rsqrt) may flip by one ulp, and
+    # that ulp carried through the second rounding, bf16(w * t), is at most two ulps of normed
+    n, ref = cpu(normed).float(), rn.float()
+    assert (n == ref).float().mean() > 0.995
+    assert bool(((n - ref).abs() <= ref.abs() * 2.0 ** -6 + 1e-30).all())
+    # the router dots are checked on the kernel's own normed rows (float64 reference), so the
+    # normed rounding differences above do not leak into this comparison
+    l64 = cpu(normed).double() @ gw.double().T
+    lg = cpu(logits).double()
+    if lbf16:
+        exact = l64.float().to(torch.bfloat16).double()
+        assert (lg == exact).float().mean() > 0.98
+        assert bool(((lg - exact).abs() <= exact.abs() * 2.0 ** -7 + 1e-6).all())
+    else:
+        torch.testing.assert_close(lg, l64, rtol=1e-5, atol=1e-5)
+    assert rl.shape == lg.shape
+
+
+def test_moe_prologue_in_place_residual(dev):
+    g = torch.Generator().manual_seed(9)
+    hid = torch.randn(40, 512, generator=g).to(torch.bfloat16).to(dev)
+    res = torch.randn(40, 512, generator=g).to(torch.bfloat16).to(dev)
+    w = torch.ones(512, dtype=torch.bfloat16, device=dev)
+    gw = (0.1 * torch.randn(8, 512, generator=g)).to(torch.bfloat16).to(dev)
+    want = ops.moe_prologue(hid, res, w, 1e-6, gw)
+    r, n, l = ops.moe_prologue(hid, res, w, 1e-6, gw, residual_out=res)   # residual updated in place
+    assert r.data_ptr() == res.data_ptr()
+    assert torch.equal(res, want[0]) and torch.equal(n, want[1]) and torch.equal(l, want[2])
+
+
 # --------------------------------------------------------------------------- align
 @pytest.mark.parametrize("T,k,E,e_lo,n_loc,skew", [
     (1, 2, 8, 0, 8, False), (512, 2, 8, 0, 8, False), (8192, 2, 8, 0, 8, False), (4096, 6, 64, 0, 64, True),

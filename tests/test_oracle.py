@@ -364,3 +364,66 @@ def test_eplb_map_invariants():
         got = phys.reshape(-1)[sel]
         want = log2phy[l][(sel % int(count[l])).long()]
         assert torch.equal(got, want)
+
+
+# --------------------------------------------------------------------------- prologue
+def _bf16_np(x64):
+    """float64 -> nearest bf16 (ties to even), as float64."""
+    return torch.from_numpy(np.asarray(x64, dtype=np.float64)).to(torch.float32).to(torch.bfloat16).double().numpy()
+
+
+def test_prologue_matches_float64_formulation():
+    g = torch.Generator().manual_seed(0)
+    T, H, E = 64, 512, 8
+    hid = (torch.randn(T, H, generator=g) * 2).to(torch.bfloat16)
+    res = (torch.randn(T, H, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    gw = (0.05 * torch.randn(E, H, generator=g)).to(torch.bfloat16)
+    r, normed, logits = oracle.moe_prologue(hid, res, w, 1e-6, gw, logits_bf16=False)
+    # residual add: exact sum rounded once to bf16
+    r64 = res.double().numpy() + hid.double().numpy()
+    assert np.array_equal(r.double().numpy(), _bf16_np(r64))
+    # RMSNorm in float64 with the same two bf16 roundings
+    rr = r.double().numpy()
+    rs = 1 / np.sqrt((rr ** 2).mean(-1, keepdims=True) + 1e-6)
+    n64 = _bf16_np(w.double().numpy() * _bf16_np(rr * rs))
+    same = normed.double().numpy() == n64
+    assert same.mean() > 0.999
+    ulp = np.abs(n64) * 2.0 ** -7
+    assert np.all(np.abs(normed.double().numpy() - n64) <= ulp + 1e-30)
+    # fp32 logits against float64 dot products of the bf16 normed rows
+    l64 = normed.double().numpy() @ gw.double().numpy().T
+    np.testing.assert_allclose(logits.numpy(), l64, rtol=1e-5, atol=1e-6)
+
+
+def test_prologue_rmsnorm_closed_forms():
+    H = 256
+    w = torch.full((H,), 0.5).to(torch.bfloat16)
+    gw = torch.zeros(2, H, dtype=torch.bfloat16)
+    gw[0] = 1.0
+    # a constant row c: t = c / sqrt(c^2 + eps) -> +-1 for eps = 0; normed = w * sign(c)
+    hid = torch.zeros(3, H, dtype=torch.bfloat16)
+    res = torch.tensor([[3.0], [-0.25], [7.0]]).expand(3, H).to(torch.bfloat16).contiguous()
+    _, normed, logits = oracle.moe_prologue(hid, res, w, 0.0, gw, logits_bf16=False)
+    assert torch.equal(normed[0], w) and torch.equal(normed[1], -w)
+    assert float(logits[0, 0]) == H * 0.5 and float(logits[0, 1]) == 0.0
+    # scale invariance: doubling a row (exact in bf16) leaves the normed row unchanged
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(4, H, generator=g).to(torch.bfloat16)
+    _, n1, _ = oracle.moe_prologue(torch.zeros_like(x), x, w, 0.0, gw)
+    _, n2, _ = oracle.moe_prologue(torch.zeros_like(x), x * 2, w, 0.0, gw)
+    assert torch.equal(n1, n2)
+
+
+def test_prologue_bf16_logits_are_rounded_fp32_dots():
+    g = torch.Generator().manual_seed(2)
+    T, H, E = 32, 256, 16
+    hid = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    res = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = torch.ones(H, dtype=torch.bfloat16)
+    gw = (0.1 * torch.randn(E, H, generator=g)).to(torch.bfloat16)
+    _, normed, lb = oracle.moe_prologue(hid, res, w, 1e-6, gw, logits_bf16=True)
+    l64 = normed.double().numpy() @ gw.double().numpy().T
+    exact = _bf16_np(l64)
+    assert (lb.double().numpy() == exact).mean() > 0.99
+    assert np.all(np.abs(lb.double().numpy() - exact) <= np.abs(exact) * 2.0 ** -7 + 1e-30)
