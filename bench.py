@@ -256,6 +256,25 @@ def gate_case(torch, ops, steps, warmup, flush):
             "hbm_frac_cold": round(nbytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def prologue_case(torch, ops, steps, warmup, flush, T, H, E, logits_bf16, name):
+    """Residual add + RMSNorm + router logits (HBM-bound: two rows in, two rows out)."""
+    g = torch.Generator(device="cuda").manual_seed(T + E)
+    hid = torch.randn(T, H, device="cuda", generator=g).to(torch.bfloat16)
+    res = torch.randn(T, H, device="cuda", generator=g).to(torch.bfloat16)
+    w = torch.ones(H, device="cuda", dtype=torch.bfloat16)
+    gw = (0.02 * torch.randn(E, H, device="cuda", generator=g)).to(torch.bfloat16)
+    ws = torch.empty(max(ops.moe_prologue_workspace_bytes(T, H, E), 1), dtype=torch.uint8, device="cuda")
+    fn = lambda: ops.moe_prologue(hid, res, w, 1e-6, gw, logits_bf16, workspace=ws)
+    settle(fn, warmup, torch)
+    ms = timed(fn, steps, warmup, torch)
+    ms_cold = timed_cold(fn, steps, 1, torch, flush)
+    nbytes = 4 * T * H * 2 + T * E * 4 + E * H * 2
+    return {"case": f"MoE prologue (residual add + RMSNorm + router) {name} T={T} H={H} E={E}", "tokens": T,
+            "ms": round(ms, 4), "ms_cold": round(ms_cold, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+            "hbm_GBps_cold": round(nbytes / (ms_cold * 1e-3) / 1e9, 1),
+            "hbm_frac_cold": round(nbytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def suite(torch, ops, mix_inp, steps, warmup):
     """The other workloads of the layer, one GPU each: timings only (parity is in tests/)."""
     from easyinfra_amd.workloads import SHAPES, make_inputs
@@ -283,6 +302,8 @@ def suite(torch, ops, mix_inp, steps, warmup):
                           ops, steps, warmup, flush, router_kw=v3))
     del ds_inp
     out.append(gate_case(torch, ops, steps, warmup, flush))
+    out.append(prologue_case(torch, ops, steps, warmup, flush, 8192, 4096, 8, True, "Mixtral-8x7B"))
+    out.append(prologue_case(torch, ops, steps, warmup, flush, 4096, 7168, 256, False, "DeepSeek-V3"))
     qw = SHAPES["qwen3-30b-a3b-local32"]
     for T in (1, 32, 256, 2048):
         hot = layer_case(f"qwen3-30b-a3b local 32/128 T={T} hot:cold 8:1", make_inputs(qw, T, device=dev), torch, ops,

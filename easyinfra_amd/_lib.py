@@ -30,7 +30,7 @@ SIGNATURES = {
     "eimoe_router_grouped_topk": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int, c_float,
                                           c_void_p, c_void_p, c_void_p]),
     "eimoe_eplb_map": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
-    "eimoe_moe_prologue_workspace_bytes": (c_size_t, []),
+    "eimoe_moe_prologue_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "eimoe_moe_prologue": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_int, c_int, c_int, c_int,
                                    c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "eimoe_align": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,

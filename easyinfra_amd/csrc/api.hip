@@ -582,7 +582,7 @@ int eimoe_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, 
   return hip_check(launch_quantize_rows_fp8(x, dtype, rows, cols, q, scale, S(stream)), "quantize_rows_fp8");
 }
 
-size_t eimoe_moe_prologue_workspace_bytes(void) { return 256; }
+size_t eimoe_moe_prologue_workspace_bytes(int T, int H, int E) { return prologue_workspace_bytes(T, H, E); }
 
 int eimoe_moe_prologue(const void* hidden, const void* residual, const void* norm_w, float eps, const void* gate_w,
                        int T, int H, int E, int flags, void* residual_out, void* normed, float* logits,
@@ -607,12 +607,11 @@ int eimoe_moe_prologue(const void* hidden, const void* residual, const void* nor
     return fail(EIMOE_ERR_SHAPE, "normed must not alias the residual or hidden rows");
   if (!fused) {
     REQUIRE_PTR(workspace);
-    if (workspace_bytes < eimoe_moe_prologue_workspace_bytes())
-      return fail(EIMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes,
-                  eimoe_moe_prologue_workspace_bytes());
+    const size_t need = prologue_workspace_bytes(T, H, E);
+    if (workspace_bytes < need) return fail(EIMOE_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, need);
   }
   return hip_check(launch_moe_prologue(hidden, residual, norm_w, eps, gate_w, T, H, E, (flags & EIMOE_LOGITS_BF16) ? 1 : 0,
-                                       residual_out, normed, logits, static_cast<int32_t*>(workspace), S(stream)),
+                                       residual_out, normed, logits, workspace, S(stream)),
                    "moe_prologue");
 }
 

@@ -61,14 +61,22 @@ hipError_t launch_route_align(const float* logits, int T, int E, int k, int reno
 hipError_t launch_counts_to_offsets(const int32_t* counts, int S, int32_t* offsets, hipStream_t s);
 // MoE prologue: residual add + RMSNorm (+ router logits).  Routers of at most
 // kPrologueFusedMaxE experts and kPrologueFusedMaxGate bytes of gate weights are dotted in
-// the same pass; others (E % 64 == 0) go through the grouped GEMM with seg_off[2] as the
-// one dense segment.
+// the same pass; others (E % 64 == 0) go through the grouped GEMM with the T rows as one
+// dense segment, H split over up to kPrologueMaxSplit fp32 planes that a last kernel sums.
+// The workspace holds the segment offsets (256 bytes) and the planes.
 constexpr int kPrologueFusedMaxE = 32;
 constexpr long long kPrologueFusedMaxGate = 128 * 1024;
+constexpr int kPrologueMaxSplit = 8;
+struct PrologueGemm {
+  int tile;
+  int k_split;
+};
 bool prologue_fused_router(int H, int E);
+PrologueGemm prologue_router_gemm(int T, int H, int E);
+size_t prologue_workspace_bytes(int T, int H, int E);
 hipError_t launch_moe_prologue(const void* hidden, const void* residual, const void* norm_w, float eps,
                                const void* gate_w, int T, int H, int E, int logits_bf16, void* res_out, void* normed,
-                               float* logits, int32_t* seg_off, hipStream_t s);
+                               float* logits, void* workspace, hipStream_t s);
 
 hipError_t launch_gather_rows(const void* x, int row_bytes, const int32_t* rows, const int32_t* num_rows,
                               int max_rows, void* xs, hipStream_t s);

@@ -33,167 +33,267 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// VPL: 16-byte vectors (8 bf16) per lane; EF: fuse the router dots (gate staged in LDS).
-template <int VPL, bool EF>
+__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t w) { return __builtin_bit_cast(bf16x2_t, w); }
+
+__device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Sums each of the EP values over the wave, halving the set at each exchange: EP/2 + EP/4 +
+// ... + 1 exchanges until a lane holds one value, then plain butterflies (EP + 5 - log2 EP
+// exchanges in all, against 6 EP for one wave sum per value).  Lane l returns the total of
+// d[l / (64 / EP)].
+template <int EP>
+__device__ __forceinline__ float wave_sum_scatter(float (&d)[EP], int lane) {
+  int n = EP;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    if (n > 1) {
+      const bool up = (lane & m) != 0;
+      const int h = n / 2;
+#pragma unroll
+      for (int i = 0; i < h; ++i) {
+        const float send = up ? d[i] : d[h + i];
+        const float keep = up ? d[h + i] : d[i];
+        d[i] = keep + __shfl_xor(send, m, 64);
+      }
+      n = h;
+    } else {
+      d[0] += __shfl_xor(d[0], m, 64);
+    }
+  }
+  return d[0];
+}
+
+// VPL: 16-byte vectors (8 bf16) per lane.  EP > 0 fuses the router dots (gate staged in LDS)
+// for up to EP experts (a power of two); EP == 0 leaves the router to the GEMM.
+// PF: the next row's loads are issued before the current row is processed.
+// seg_off (the router GEMM's one segment, [0, T]) is written by the first thread when given.
+template <int VPL, int EP, bool PF>
 __global__ __launch_bounds__(kProThreads) void prologue_kernel(
     const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ residual, const uint16_t* __restrict__ norm_w,
     float eps, const uint16_t* __restrict__ gate_w, int T, int H, int E, int logits_bf16,
-    uint16_t* __restrict__ res_out, uint16_t* __restrict__ normed, float* __restrict__ logits) {
+    uint16_t* __restrict__ res_out, uint16_t* __restrict__ normed, float* __restrict__ logits,
+    int32_t* __restrict__ seg_off) {
+  constexpr bool EF = EP > 0;
   extern __shared__ uint4 s_gate[];   // [E][H/8] when EF
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int nvec = H / 8;
+  if (seg_off != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    seg_off[0] = 0;
+    seg_off[1] = T;
+  }
   if constexpr (EF) {
     const uint4* g = reinterpret_cast<const uint4*>(gate_w);
     for (int i = threadIdx.x; i < E * nvec; i += kProThreads) s_gate[i] = g[i];
     __syncthreads();
   }
-  uint4 wv8[VPL];   // RMSNorm weight, the same for every row
+  const uint4* wr = reinterpret_cast<const uint4*>(norm_w);
+  uint4 wv8[EF ? VPL : 1];   // RMSNorm weight, kept across rows when the grid is persistent
+  if constexpr (EF) {
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int v = j * 64 + lane;
-    wv8[j] = v < nvec ? reinterpret_cast<const uint4*>(norm_w)[v] : make_uint4(0u, 0u, 0u, 0u);
+    for (int j = 0; j < VPL; ++j) {
+      const int v = j * 64 + lane;
+      wv8[j] = v < nvec ? wr[v] : make_uint4(0u, 0u, 0u, 0u);
+    }
   }
-  for (int t = blockIdx.x * kProWaves + wv; t < T; t += gridDim.x * kProWaves) {
+  const int stride = gridDim.x * kProWaves;
+  auto load_row = [&](int t, uint4 (&a)[VPL], uint4 (&b)[VPL]) {
     const uint4* hr = reinterpret_cast<const uint4*>(hidden + static_cast<long long>(t) * H);
     const uint4* rr = reinterpret_cast<const uint4*>(residual + static_cast<long long>(t) * H);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int v = j * 64 + lane;
+      a[j] = v < nvec ? hr[v] : make_uint4(0u, 0u, 0u, 0u);
+      b[j] = v < nvec ? rr[v] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  uint4 ha[VPL], rb[VPL], hn[PF ? VPL : 1], rn[PF ? VPL : 1];
+  int t = blockIdx.x * kProWaves + wv;
+  if constexpr (PF) {
+    if (t < T) load_row(t, ha, rb);
+  }
+  for (; t < T; t += stride) {
+    if constexpr (PF) {
+      if (t + stride < T) load_row(t + stride, hn, rn);
+    } else {
+      load_row(t, ha, rb);
+    }
+    // r = bf16(residual + hidden), held in ha from here on
     uint4* ro = reinterpret_cast<uint4*>(res_out + static_cast<long long>(t) * H);
-    uint4 r8[VPL];
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       const int v = j * 64 + lane;
-      r8[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (v < nvec) {
-        const uint4 a = hr[v], b = rr[v];
-        const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-        uint32_t o[4];
+      uint32_t aw[4] = {ha[j].x, ha[j].y, ha[j].z, ha[j].w};
+      const uint32_t bw[4] = {rb[j].x, rb[j].y, rb[j].z, rb[j].w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float lo = bf16_to_f32(static_cast<uint16_t>(bw[q])) + bf16_to_f32(static_cast<uint16_t>(aw[q]));
-          const float hi = bf16_to_f32(static_cast<uint16_t>(bw[q] >> 16)) + bf16_to_f32(static_cast<uint16_t>(aw[q] >> 16));
-          o[q] = pack_bf16x2(lo, hi);
-          const float rl = bf16_to_f32(static_cast<uint16_t>(o[q])), rh = bf16_to_f32(static_cast<uint16_t>(o[q] >> 16));
-          ss += rl * rl + rh * rh;
-        }
-        r8[j] = make_uint4(o[0], o[1], o[2], o[3]);
-        ro[v] = r8[j];
+      for (int q = 0; q < 4; ++q) {
+        aw[q] = pack_bf16x2(lo_f32(bw[q]) + lo_f32(aw[q]), hi_f32(bw[q]) + hi_f32(aw[q]));
+        const float rl = lo_f32(aw[q]), rh = hi_f32(aw[q]);
+        ss += rl * rl + rh * rh;
       }
+      ha[j] = make_uint4(aw[0], aw[1], aw[2], aw[3]);
+      if (v < nvec) ro[v] = ha[j];
     }
     const float rs = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(H) + eps);
+    // normed = bf16(weight * bf16(r * rs)), held in ha from here on
     uint4* no = reinterpret_cast<uint4*>(normed + static_cast<long long>(t) * H);
-    // normed = bf16(weight * bf16(r * rs)); router dots against the staged gate rows
-    uint4 n8[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       const int v = j * 64 + lane;
-      const uint32_t rw[4] = {r8[j].x, r8[j].y, r8[j].z, r8[j].w};
-      const uint32_t ww[4] = {wv8[j].x, wv8[j].y, wv8[j].z, wv8[j].w};
-      uint32_t o[4];
+      uint4 w8;
+      if constexpr (EF) w8 = wv8[j];
+      else w8 = v < nvec ? wr[v] : make_uint4(0u, 0u, 0u, 0u);
+      uint32_t rw[4] = {ha[j].x, ha[j].y, ha[j].z, ha[j].w};
+      const uint32_t ww[4] = {w8.x, w8.y, w8.z, w8.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float tl = bf16_to_f32(f32_to_bf16(bf16_to_f32(static_cast<uint16_t>(rw[q])) * rs));
-        const float th = bf16_to_f32(f32_to_bf16(bf16_to_f32(static_cast<uint16_t>(rw[q] >> 16)) * rs));
-        o[q] = pack_bf16x2(bf16_to_f32(static_cast<uint16_t>(ww[q])) * tl,
-                           bf16_to_f32(static_cast<uint16_t>(ww[q] >> 16)) * th);
+        const uint32_t tq = pack_bf16x2(lo_f32(rw[q]) * rs, hi_f32(rw[q]) * rs);
+        rw[q] = pack_bf16x2(lo_f32(ww[q]) * lo_f32(tq), hi_f32(ww[q]) * hi_f32(tq));
       }
-      n8[j] = make_uint4(o[0], o[1], o[2], o[3]);
-      if (v < nvec) no[v] = n8[j];
+      ha[j] = make_uint4(rw[0], rw[1], rw[2], rw[3]);
+      if (v < nvec) no[v] = ha[j];
     }
     if constexpr (EF) {
-      float mine = 0.f;
-#pragma unroll 1
-      for (int e = 0; e < E; ++e) {
-        float d = 0.f;
+      // router dots against the staged gate rows, two bf16 products per v_dot2 (fp32 sums)
+      float d[EP];
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-          const int v = j * 64 + lane;
-          if (v < nvec) {
-            const uint4 gq = s_gate[e * nvec + v];
-            const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
-            const uint32_t nw[4] = {n8[j].x, n8[j].y, n8[j].z, n8[j].w};
+      for (int e = 0; e < EP; ++e) {
+        d[e] = 0.f;
+        if (e < E) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              d += bf16_to_f32(static_cast<uint16_t>(nw[q])) * bf16_to_f32(static_cast<uint16_t>(gw[q]));
-              d += bf16_to_f32(static_cast<uint16_t>(nw[q] >> 16)) * bf16_to_f32(static_cast<uint16_t>(gw[q] >> 16));
+          for (int j = 0; j < VPL; ++j) {
+            const int v = j * 64 + lane;
+            if (v < nvec) {
+              const uint4 gq = s_gate[e * nvec + v];
+              d[e] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(ha[j].x), as_bf16x2(gq.x), d[e], false);
+              d[e] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(ha[j].y), as_bf16x2(gq.y), d[e], false);
+              d[e] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(ha[j].z), as_bf16x2(gq.z), d[e], false);
+              d[e] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(ha[j].w), as_bf16x2(gq.w), d[e], false);
             }
           }
         }
-        d = wave_sum(d);
-        if (lane == e) mine = d;
       }
-      if (lane < E)
-        logits[static_cast<long long>(t) * E + lane] = logits_bf16 ? bf16_to_f32(f32_to_bf16(mine)) : mine;
+      const float tot = wave_sum_scatter<EP>(d, lane);
+      constexpr int kSpan = 64 / EP;   // lanes holding each expert's total
+      const int e = lane / kSpan;
+      if (lane % kSpan == 0 && e < E)
+        logits[static_cast<long long>(t) * E + e] = logits_bf16 ? bf16_to_f32(f32_to_bf16(tot)) : tot;
+    }
+    if constexpr (PF) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        ha[j] = hn[j];
+        rb[j] = rn[j];
+      }
     }
   }
 }
 
-__global__ void round_bf16_kernel(float* __restrict__ x, long long n) {
+// logits = sum of the K-split planes in order (and rounded to bf16 values when asked)
+// (in place when n_split == 1 and planes == out)
+__global__ void sum_planes_kernel(const float* planes, int n_split, long long n, int round, float* out) {
   for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n;
-       i += static_cast<long long>(gridDim.x) * 256)
-    x[i] = bf16_to_f32(f32_to_bf16(x[i]));
-}
-
-__global__ void one_segment_kernel(int32_t* off, int T) {
-  if (threadIdx.x == 0) {
-    off[0] = 0;
-    off[1] = T;
+       i += static_cast<long long>(gridDim.x) * 256) {
+    float v = planes[i];
+    for (int s = 1; s < n_split; ++s) v += planes[static_cast<long long>(s) * n + i];
+    out[i] = round ? bf16_to_f32(f32_to_bf16(v)) : v;
   }
 }
 
-template <int VPL, bool EF>
+template <int VPL, int EP, bool PF>
 hipError_t launch_prologue_v(const void* hidden, const void* residual, const void* norm_w, float eps,
                              const void* gate_w, int T, int H, int E, int logits_bf16, void* res_out, void* normed,
-                             float* logits, hipStream_t s) {
-  const size_t lds = EF ? static_cast<size_t>(E) * H * 2 : 0;
+                             float* logits, int32_t* seg_off, hipStream_t s) {
+  const size_t lds = EP ? static_cast<size_t>(E) * H * 2 : 0;
   if (lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(prologue_kernel<VPL, EF>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(prologue_kernel<VPL, EP, PF>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return e;
   }
   // fused: a persistent grid amortises staging the gate (2 workgroups per CU); else a wave per row
   long long grid = (T + kProWaves - 1) / kProWaves;
-  if (EF && grid > 2ll * kNumCu) grid = 2ll * kNumCu;
+  if (EP && grid > 2ll * kNumCu) grid = 2ll * kNumCu;
   if (grid < 1) grid = 1;
-  hipLaunchKernelGGL((prologue_kernel<VPL, EF>), dim3(static_cast<unsigned>(grid)), dim3(kProThreads), lds, s,
+  hipLaunchKernelGGL((prologue_kernel<VPL, EP, PF>), dim3(static_cast<unsigned>(grid)), dim3(kProThreads), lds, s,
                      static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(residual),
                      static_cast<const uint16_t*>(norm_w), eps, static_cast<const uint16_t*>(gate_w), T, H, E,
-                     logits_bf16, static_cast<uint16_t*>(res_out), static_cast<uint16_t*>(normed), logits);
+                     logits_bf16, static_cast<uint16_t*>(res_out), static_cast<uint16_t*>(normed), logits, seg_off);
   return hipGetLastError();
 }
 
-template <bool EF>
+// The fused kernel loops over rows and prefetches the next one where the registers allow it.
+template <int EP>
 hipError_t launch_prologue_e(int vpl, const void* hidden, const void* residual, const void* norm_w, float eps,
                              const void* gate_w, int T, int H, int E, int logits_bf16, void* res_out, void* normed,
-                             float* logits, hipStream_t s) {
-#define EIMOE_PRO(V) \
-  return launch_prologue_v<V, EF>(hidden, residual, norm_w, eps, gate_w, T, H, E, logits_bf16, res_out, normed, \
-                                  logits, s)
-  if (vpl <= 1) EIMOE_PRO(1);
-  if (vpl <= 2) EIMOE_PRO(2);
-  if (vpl <= 4) EIMOE_PRO(4);
-  if (vpl <= 8) EIMOE_PRO(8);
-  EIMOE_PRO(16);
+                             float* logits, int32_t* seg_off, hipStream_t s) {
+#define EIMOE_PRO(V, PF) \
+  return launch_prologue_v<V, EP, PF>(hidden, residual, norm_w, eps, gate_w, T, H, E, logits_bf16, res_out, normed, \
+                                      logits, seg_off, s)
+  if (vpl <= 1) EIMOE_PRO(1, (EP > 0));
+  if (vpl <= 2) EIMOE_PRO(2, (EP > 0));
+  if (vpl <= 4) EIMOE_PRO(4, (EP > 0));
+  if (vpl <= 8) EIMOE_PRO(8, (EP > 0 && EP <= 16));
+  EIMOE_PRO(16, false);
 #undef EIMOE_PRO
+}
+
+hipError_t launch_prologue_fused(int vpl, const void* hidden, const void* residual, const void* norm_w, float eps,
+                                 const void* gate_w, int T, int H, int E, int logits_bf16, void* res_out,
+                                 void* normed, float* logits, hipStream_t s) {
+#define EIMOE_PRO_E(P)                                                                                              \
+  return launch_prologue_e<P>(vpl, hidden, residual, norm_w, eps, gate_w, T, H, E, logits_bf16, res_out, normed, \
+                              logits, nullptr, s)
+  if (E <= 1) EIMOE_PRO_E(1);
+  if (E <= 2) EIMOE_PRO_E(2);
+  if (E <= 4) EIMOE_PRO_E(4);
+  if (E <= 8) EIMOE_PRO_E(8);
+  if (E <= 16) EIMOE_PRO_E(16);
+  EIMOE_PRO_E(32);
+#undef EIMOE_PRO_E
 }
 
 }  // namespace
 
 bool prologue_fused_router(int H, int E) { return E <= kPrologueFusedMaxE && 2ll * E * H <= kPrologueFusedMaxGate; }
 
+// Router GEMM shape for the non-fused path: 128x128 tiles from 512 rows on when E allows (else
+// 16x64), and the K dimension (H) split into fp32 planes, each at least 512 deep, until there
+// are two tiles per CU (4096 x 256 x 7168: 64 tiles, 8 planes: 24 us against 28 us with 4 and
+// 73 us unsplit, measured on MI355X).
+PrologueGemm prologue_router_gemm(int T, int H, int E) {
+  PrologueGemm g{};
+  const bool m_tile = E % 128 == 0 && T >= 512;
+  g.tile = m_tile ? kTileM : kTileXS;
+  const long long tiles = ((T + (m_tile ? 127 : 15)) / (m_tile ? 128 : 16)) * static_cast<long long>(E / (m_tile ? 128 : 64));
+  g.k_split = 1;
+  while (g.k_split < kPrologueMaxSplit && tiles * g.k_split < 2ll * kNumCu && H % (128 * g.k_split) == 0 &&
+         H / (2 * g.k_split) >= 512)
+    g.k_split *= 2;
+  return g;
+}
+
+size_t prologue_workspace_bytes(int T, int H, int E) {
+  if (T < 0 || H < 1 || E < 1 || prologue_fused_router(H, E)) return 0;
+  const PrologueGemm g = prologue_router_gemm(T, H, E);
+  return 256 + (g.k_split > 1 ? static_cast<size_t>(g.k_split) * T * E * sizeof(float) : 0);
+}
+
 hipError_t launch_moe_prologue(const void* hidden, const void* residual, const void* norm_w, float eps,
                                const void* gate_w, int T, int H, int E, int logits_bf16, void* res_out, void* normed,
-                               float* logits, int32_t* seg_off, hipStream_t s) {
+                               float* logits, void* workspace, hipStream_t s) {
   const int vpl = (H / 8 + 63) / 64;
   if (prologue_fused_router(H, E))
-    return launch_prologue_e<true>(vpl, hidden, residual, norm_w, eps, gate_w, T, H, E, logits_bf16, res_out, normed,
-                                   logits, s);
-  hipError_t e = launch_prologue_e<false>(vpl, hidden, residual, norm_w, eps, gate_w, T, H, E, logits_bf16, res_out,
-                                          normed, logits, s);
-  if (e != hipSuccess) return e;
+    return launch_prologue_fused(vpl, hidden, residual, norm_w, eps, gate_w, T, H, E, logits_bf16, res_out, normed,
+                                 logits, s);
   // router GEMM: the T normed rows as one segment against the [E, H] gate, fp32 out
-  hipLaunchKernelGGL(one_segment_kernel, dim3(1), dim3(64), 0, s, seg_off, T);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  int32_t* seg_off = static_cast<int32_t*>(workspace);
+  hipError_t e = launch_prologue_e<0>(vpl, hidden, residual, norm_w, eps, gate_w, T, H, E, logits_bf16, res_out,
+                                          normed, logits, seg_off, s);
+  if (e != hipSuccess) return e;
+  const PrologueGemm g = prologue_router_gemm(T, H, E);
+  float* planes = g.k_split > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + 256) : logits;
   GemmArgs p{};
   p.a = normed;
   p.lda = H;
@@ -202,21 +302,23 @@ hipError_t launch_moe_prologue(const void* hidden, const void* residual, const v
   p.ldb = H;
   p.nb_rows = E;
   p.N = E;
-  p.K = H;
+  p.K = H / g.k_split;
   p.seg_off = seg_off;
   p.S = 1;
   p.e_mod = 1;
-  p.c = logits;
+  p.c = planes;
   p.ldc = E;
-  p.k_split = 1;
+  p.c_split_stride = static_cast<long long>(T) * E;
+  p.k_split = g.k_split;
   p.max_rows = T;
   p.a_rows_cap = T;
-  if ((e = launch_grouped_gemm(p, kEpiStoreF32, false, false, T, kTileAuto, s)) != hipSuccess) return e;
-  if (logits_bf16) {
+  if ((e = launch_grouped_gemm(p, kEpiStoreF32, false, false, T, g.tile, s)) != hipSuccess) return e;
+  if (g.k_split > 1 || logits_bf16) {
     const long long n = static_cast<long long>(T) * E;
     long long blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(round_bf16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, logits, n);
+    hipLaunchKernelGGL(sum_planes_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, planes, g.k_split, n,
+                       logits_bf16, logits);
     e = hipGetLastError();
   }
   return e;

@@ -74,13 +74,19 @@ def moe_prologue(hidden: torch.Tensor, residual: torch.Tensor, norm_w: torch.Ten
     res_out = torch.empty_like(residual) if residual_out is None else residual_out
     normed = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     logits = torch.empty(T, E, dtype=torch.float32, device=dev)
-    need = int(_lib.lib().eimoe_moe_prologue_workspace_bytes())
-    if workspace is None or workspace.numel() < need:
+    need = moe_prologue_workspace_bytes(T, H, E)
+    if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     call("eimoe_moe_prologue", hidden.data_ptr(), residual.data_ptr(), norm_w.data_ptr(), float(eps),
          gate_w.data_ptr(), T, H, E, _lib.LOGITS_BF16 if logits_bf16 else 0, res_out.data_ptr(), normed.data_ptr(),
-         logits.data_ptr(), workspace.data_ptr(), workspace.numel(), _stream(hidden))
+         logits.data_ptr(), _ptr(workspace), 0 if workspace is None else workspace.numel(), _stream(hidden))
     return res_out, normed, logits
+
+
+def moe_prologue_workspace_bytes(T: int, H: int, E: int) -> int:
+    """Workspace bytes ``moe_prologue`` needs at these sizes (0 when the router is dotted in the
+    same pass; else the router GEMM's segment offsets and K-split planes)."""
+    return int(_lib.lib().eimoe_moe_prologue_workspace_bytes(T, H, E))
 
 
 def router_grouped_topk(logits: torch.Tensor, top_k: int, n_group: int = 1, topk_group: int = 1,

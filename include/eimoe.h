@@ -196,10 +196,11 @@ int eimoe_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, 
  * models/deepseek_v3/modeling_deepseek_v3.py:155-157).
  *   hidden, residual, residual_out, normed [T,H] bf16; norm_w [H] bf16; gate_w [E,H] bf16;
  *   logits [T,E] fp32.  64 <= H <= 8192, H % 64 == 0; E <= 32 with E*H*2 <= 128 KiB (one pass),
- *   or E % 64 == 0 up to EIMOE_MAX_EXPERTS (router GEMM on the MFMA, needs the workspace).
+ *   or E % 64 == 0 up to EIMOE_MAX_EXPERTS (router GEMM on the MFMA, needs the workspace:
+ *   eimoe_moe_prologue_workspace_bytes(T, H, E) bytes, 0 for the one-pass routers).
  *   residual_out may alias residual; normed may not alias residual_out. */
 enum { EIMOE_LOGITS_BF16 = 1 };
-size_t eimoe_moe_prologue_workspace_bytes(void);
+size_t eimoe_moe_prologue_workspace_bytes(int T, int H, int E);
 int eimoe_moe_prologue(const void* hidden, const void* residual, const void* norm_w, float eps, const void* gate_w,
                        int T, int H, int E, int flags, void* residual_out, void* normed, float* logits,
                        void* workspace, size_t workspace_bytes, void* stream);

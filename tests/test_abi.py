@@ -92,6 +92,13 @@ def test_moe_prologue_validation():
     assert _rc(f, None, None, None, 1e-6, None, 4, 4096, 48, 0, *n, None, 0, None) == _lib.ERR_SHAPE  # 48 experts
     assert _rc(f, None, None, None, 1e-6, None, 4, 4096, 8, 0, *n, None, 0, None) == _lib.ERR_NULL
     assert _rc(f, None, None, None, 1e-6, None, 0, 4096, 8, 0, *n, None, 0, None) == _lib.EIMOE_OK
+    # the router GEMM's workspace: offsets, then K-split planes while the tiles do not fill the chip
+    ws = _lib.lib().eimoe_moe_prologue_workspace_bytes
+    assert ws(8192, 4096, 8) == 0                                    # dotted in the same pass
+    assert ws(4096, 7168, 256) == 256 + 8 * 4096 * 256 * 4           # 64 tiles of 128 x 128: 8 planes
+    assert ws(16384, 2048, 128) == 256 + 4 * 16384 * 128 * 4         # 128 tiles: 4 planes of 512
+    assert ws(4100, 1024, 192) == 256                                # 771 tiles of 16 x 64: no split
+    assert _rc(f, 1, 1, 1, 1e-6, 1, 4096, 7168, 256, 0, 1, 2, 3, 4, 256, None) == _lib.ERR_WORKSPACE
 
 
 def test_gemm_validation():

@@ -108,10 +108,12 @@ def test_eplb_map_matches_oracle(dev, L, ep, P, T, k):
 
 # --------------------------------------------------------------------------- MoE prologue
 # One pass for small routers (gate staged in LDS; the 8 x 7168 gate is 114 KiB), the MFMA
-# router GEMM for E a multiple of 64 (Qwen3 128, DeepSeek-V3 256).
+# router GEMM for E a multiple of 64 (Qwen3 128, DeepSeek-V3 256), its H split into 1-8 fp32
+# planes (4096 x 256: 8 planes; 257 x 256 in 16 x 64 tiles: 8; 16384 x 128: 4; 4100 x 192: none).
 @pytest.mark.parametrize("T,H,E,lbf16", [(1, 4096, 8, True), (300, 4096, 8, True), (257, 2048, 16, True),
                                          (64, 7168, 8, False), (33, 64, 32, True), (100, 2048, 128, True),
-                                         (257, 7168, 256, False), (1, 4096, 64, True)])
+                                         (257, 7168, 256, False), (1, 4096, 64, True), (4096, 7168, 256, False),
+                                         (16384, 2048, 128, True), (8192, 4096, 8, True), (4100, 1024, 192, False)])
 def test_moe_prologue_matches_oracle(dev, T, H, E, lbf16):
     g = torch.Generator().manual_seed(T + H + E)
     hid = (torch.randn(T, H, generator=g) * 2).to(torch.bfloat16)
