@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--no-suite", action="store_true",
                     help="skip the other workloads (tiny fp32 layer, DeepSeek-V2-Lite, Qwen3-30B-A3B local share, "
                          "fp8 Mixtral)")
-    ap.add_argument("--profile-case", default=None, metavar="NAME:T[:uniform][:w8a8]",
+    ap.add_argument("--profile-case", default=None, metavar="NAME:T[:uniform][:w8a8] | prologue:T:H:E[:f32]",
                     help="profiling driver: 12 cache-flushed fused-layer calls of one workload (names as in "
                          "easyinfra_amd.workloads.SHAPES); prints no JSON line")
     ap.add_argument("--traffic-run", action="store_true",
@@ -326,6 +326,21 @@ def suite(torch, ops, mix_inp, steps, warmup):
 def profile_case(torch, ops, spec):
     from easyinfra_amd.workloads import SHAPES, make_inputs
     parts = spec.split(":")
+    if parts[0] == "prologue":   # prologue:T:H:E[:f32] -- residual add + RMSNorm + router logits
+        T, H, E = (int(v) for v in parts[1:4])
+        g = torch.Generator(device="cuda").manual_seed(T + E)
+        hid = torch.randn(T, H, device="cuda", generator=g).to(torch.bfloat16)
+        res = torch.randn(T, H, device="cuda", generator=g).to(torch.bfloat16)
+        w = torch.ones(H, device="cuda", dtype=torch.bfloat16)
+        gw = (0.02 * torch.randn(E, H, device="cuda", generator=g)).to(torch.bfloat16)
+        ws = torch.empty(max(ops.moe_prologue_workspace_bytes(T, H, E), 1), dtype=torch.uint8, device="cuda")
+        flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+        for _ in range(12):
+            flush.sum()
+            ops.moe_prologue(hid, res, w, 1e-6, gw, "f32" not in parts[4:], workspace=ws)
+        torch.cuda.synchronize()
+        print("profile case done:", spec, flush=True)
+        return
     shape, T = SHAPES[parts[0]], int(parts[1])
     inp = make_inputs(shape, T, device="cuda", uniform_twin="uniform" in parts[2:])
     wgu, wd, scales = inp.w_gate_up.to(torch.bfloat16), inp.w_down.to(torch.bfloat16), None
