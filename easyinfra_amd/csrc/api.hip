@@ -595,6 +595,8 @@ int eimoe_moe_prologue(const void* hidden, const void* residual, const void* nor
     return fail(EIMOE_ERR_SHAPE, "E=%d: up to %d experts with %lld bytes of gate weights, or a multiple of 64", E,
                 kPrologueFusedMaxE, kPrologueFusedMaxGate);
   if (!(eps >= 0.f)) return fail(EIMOE_ERR_SHAPE, "eps must be >= 0");
+  if (!fused && static_cast<long long>(T) * H * 2 > 0x7fffffffll)   // the router GEMM's 32-bit buffer offsets
+    return fail(EIMOE_ERR_SHAPE, "normed (%d rows x %d) exceeds 2 GiB", T, H);
   if (T == 0) return EIMOE_OK;
   REQUIRE_PTR(hidden);
   REQUIRE_PTR(residual);
@@ -643,6 +645,17 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   if ((flags & EIMOE_W8A8) && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "EIMOE_W8A8 needs fp8 weights");
   if ((flags & EIMOE_W8A8) && (H % 128 || I % 128))
     return fail(EIMOE_ERR_ALIGN, "W8A8 needs H=%d and I=%d multiples of 128", H, I);
+  {
+    // The GEMMs address x, h and one expert's weights through 32-bit buffer offsets.
+    const long long wb = w_dtype == EIMOE_FP8 ? 1 : 2;
+    if (static_cast<long long>(T) * H * 2 > 0x7fffffffll)
+      return fail(EIMOE_ERR_SHAPE, "x (%d rows x %d) exceeds 2 GiB", T, H);
+    if (static_cast<long long>(T) * k * I * 2 > 0x7fffffffll)
+      return fail(EIMOE_ERR_SHAPE, "h (%d x %d rows x %d) exceeds 2 GiB", T, k, I);
+    if (2ll * I * H * wb > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "one expert's gate/up weights exceed 2 GiB");
+    if (static_cast<long long>(T) * shared_inter * 2 > 0x7fffffffll || 2ll * shared_inter * H * 2 > 0x7fffffffll)
+      return fail(EIMOE_ERR_SHAPE, "shared experts (%d rows x %d) exceed 2 GiB", T, shared_inter);
+  }
   if (T == 0) return EIMOE_OK;
   const bool routing_in = (flags & EIMOE_ROUTING_IN) != 0;
   REQUIRE_PTR(x);

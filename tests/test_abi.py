@@ -99,6 +99,7 @@ def test_moe_prologue_validation():
     assert ws(16384, 2048, 128) == 256 + 4 * 16384 * 128 * 4         # 128 tiles: 4 planes of 512
     assert ws(4100, 1024, 192) == 256                                # 771 tiles of 16 x 64: no split
     assert _rc(f, 1, 1, 1, 1e-6, 1, 4096, 7168, 256, 0, 1, 2, 3, 4, 256, None) == _lib.ERR_WORKSPACE
+    assert _rc(f, 1, 1, 1, 1e-6, 1, 262144, 4096, 256, 0, 1, 2, 3, 4, 1 << 40, None) == _lib.ERR_SHAPE  # normed 2 GiB
 
 
 def test_gemm_validation():
@@ -156,6 +157,11 @@ def test_fused_validation_and_workspace():
     assert call(Is=256) == _lib.ERR_NULL                         # shared size without weights
     assert call(wsb=16) == _lib.ERR_WORKSPACE
     assert "workspace" in _lib.last_error()
+    # extents past the GEMMs' 32-bit buffer offsets are refused before any launch
+    assert call(T=131072, H=8192, I=128) == _lib.ERR_SHAPE        # x: 2 GiB
+    assert "x (" in _lib.last_error()
+    assert call(T=65536, H=256, I=8192, k=2) == _lib.ERR_SHAPE     # h: T*k x I = 2 GiB
+    assert call(H=8192, I=65536, T=16) == _lib.ERR_SHAPE           # one expert's gate/up weights
     assert call(T=0) == _lib.EIMOE_OK
     ws = _lib.lib().eimoe_fused_moe_workspace_bytes(16, 256, 128, 8, 2, 8, 0, _lib.BF16, 1)
     ws_sh = _lib.lib().eimoe_fused_moe_workspace_bytes(16, 256, 128, 8, 2, 8, 256, _lib.BF16, 1)
