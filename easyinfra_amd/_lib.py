@@ -33,8 +33,9 @@ SIGNATURES = {
     "eimoe_moe_prologue_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "eimoe_moe_prologue": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_int, c_int, c_int, c_int,
                                    c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "eimoe_align_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "eimoe_align": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
-                            c_void_p, c_void_p]),
+                            c_void_p, c_void_p, c_size_t, c_void_p]),
     "eimoe_route_align": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "eimoe_counts_to_offsets": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),

@@ -152,7 +152,7 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
 }
 
 struct FusedLayout {
-  size_t ids, w, counts, offsets, sorted_flat, sorted_tok, pos, h, y, sh_off, sh_h, sh_y, xq, sx, hq, sh, total;
+  size_t ids, w, counts, offsets, sorted_flat, sorted_tok, pos, hist, h, y, sh_off, sh_h, sh_y, xq, sx, hq, sh, total;
   int k_split;
   int y_dtype;
   int rows_hint;
@@ -185,6 +185,7 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   L.sorted_flat = take(A * 4);
   L.sorted_tok = take(A * 4);
   L.pos = take(A * 4);
+  L.hist = take(align_plan(static_cast<int>(A), n_local).hist_ints * 4);
   L.h = take(A * I * 2);
   L.y = take(static_cast<size_t>(L.k_split) * A * H * elem_size(L.y_dtype));
   if (flags & EIMOE_W8A8) {
@@ -328,8 +329,14 @@ int eimoe_eplb_map(const int32_t* topk_ids, int T, int k, const int32_t* log2phy
                    "eplb_map");
 }
 
+size_t eimoe_align_workspace_bytes(int T, int k, int n_local) {
+  if (T < 0 || k < 1 || n_local < 1 || static_cast<long long>(T) * k > 0x7fffffffll) return 0;
+  return align_plan(T * k, n_local).hist_ints * sizeof(int32_t);
+}
+
 int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, int32_t* counts, int32_t* offsets,
-                int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream) {
+                int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* workspace, size_t workspace_bytes,
+                void* stream) {
   if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
   if (k < 1 || k > EIMOE_MAX_TOPK) return fail(EIMOE_ERR_SHAPE, "k=%d outside [1,%d]", k, EIMOE_MAX_TOPK);
   if (n_local < 1 || n_local > EIMOE_MAX_EXPERTS)
@@ -344,7 +351,11 @@ int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, in
     REQUIRE_PTR(sorted_tok);
     REQUIRE_PTR(pos);
   }
-  return hip_check(launch_align(topk_ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos,
+  // the many-workgroup sort when the caller's workspace holds its chunk counts
+  const size_t need = eimoe_align_workspace_bytes(T, k, n_local);
+  int32_t* hist = (workspace != nullptr && need > 0 && workspace_bytes >= need) ? static_cast<int32_t*>(workspace)
+                                                                                : nullptr;
+  return hip_check(launch_align(topk_ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos, hist,
                                 S(stream)),
                    "align");
 }
@@ -371,7 +382,7 @@ int eimoe_route_align(const float* logits, int T, int E, int k, int renormalize,
     REQUIRE_PTR(pos);
   }
   return hip_check(launch_route_align(logits, T, E, k, renormalize ? 1 : 0, e_lo, n_local, topk_ids, topk_weights,
-                                      counts, offsets, sorted_flat, sorted_tok, pos, S(stream)),
+                                      counts, offsets, sorted_flat, sorted_tok, pos, nullptr, S(stream)),
                    "route_align");
 }
 
@@ -689,6 +700,7 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   int32_t* sorted_flat = static_cast<int32_t*>(at(L.sorted_flat));
   int32_t* sorted_tok = static_cast<int32_t*>(at(L.sorted_tok));
   int32_t* pos = static_cast<int32_t*>(at(L.pos));
+  int32_t* hist = static_cast<int32_t*>(at(L.hist));   // the many-workgroup align's chunk counts
   const hipStream_t s = S(stream);
   const int A = T * k;
   int rc;
@@ -733,11 +745,13 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   auto routed = [&]() -> int {
     int rc;
     if (routing_in) {
-      if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos, s),
+      if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos,
+                                       hist, s),
                           "align")))
         return rc;
     } else if ((rc = hip_check(launch_route_align(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, e_lo,
-                                                  n_local, ids, w, counts, offsets, sorted_flat, sorted_tok, pos, s),
+                                                  n_local, ids, w, counts, offsets, sorted_flat, sorted_tok, pos, hist,
+                                                  s),
                                "route_align"))) {
       return rc;
     }

@@ -726,7 +726,6 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8w_kernel(GemmA
 }
 
 // ---------------------------------------------------------------------------- launch
-
 template <int BM, int BN, int WGM, int WGN, int EPI, bool BFP8, int GM>
 static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStream_t s) {
   constexpr int OUT_BN = (EPI == kEpiSiluBF16) ? BN / 2 : BN;

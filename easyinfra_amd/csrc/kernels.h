@@ -50,14 +50,26 @@ hipError_t launch_router_grouped(const float* logits, int T, int E, int k, int n
 hipError_t launch_eplb_map(const int32_t* ids, int n, const int32_t* log2phy, int n_logical, int max_rep,
                            const int32_t* replica_count, int32_t* phys, hipStream_t s);
 size_t align_lds_bytes(int n_loc);
+// Align: one workgroup, or from kAlignMbMinIds flat ids with a hist buffer of
+// align_plan(N, n_loc).hist_ints ints, two launches over align_plan(...).blocks workgroups.
+constexpr int kAlignMbMinIds = 4096;
+constexpr int kAlignMbIdsPerBlock = 1024;
+constexpr int kAlignMbMaxBlocks = 256;
+constexpr int kAlignMbMaxCells = 16384;   // chunk-count matrix cells (blocks x n_loc)
+struct AlignPlan {
+  int blocks;   // 0: the one-workgroup kernel
+  int chunk;
+  size_t hist_ints;
+};
+AlignPlan align_plan(int N, int n_loc);
 hipError_t launch_align(const int32_t* ids, int T, int k, int e_lo, int n_loc, int32_t* counts, int32_t* offsets,
-                        int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, hipStream_t s);
+                        int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, int32_t* hist, hipStream_t s);
 // Router then align; one workgroup runs both when route_align_fused() (small batches),
 // otherwise the two kernels above.
 bool route_align_fused(int T, int E, int k, int n_loc);
 hipError_t launch_route_align(const float* logits, int T, int E, int k, int renorm, int e_lo, int n_loc,
                               int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
-                              int32_t* sorted_tok, int32_t* pos, hipStream_t s);
+                              int32_t* sorted_tok, int32_t* pos, int32_t* hist, hipStream_t s);
 hipError_t launch_counts_to_offsets(const int32_t* counts, int S, int32_t* offsets, hipStream_t s);
 // MoE prologue: residual add + RMSNorm (+ router logits).  Routers of at most
 // kPrologueFusedMaxE experts and kPrologueFusedMaxGate bytes of gate weights are dotted in

@@ -295,11 +295,11 @@ bool route_align_fused(int T, int E, int k, int n_loc) {
 
 hipError_t launch_route_align(const float* logits, int T, int E, int k, int renorm, int e_lo, int n_loc,
                               int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
-                              int32_t* sorted_tok, int32_t* pos, hipStream_t s) {
+                              int32_t* sorted_tok, int32_t* pos, int32_t* hist, hipStream_t s) {
   if (!route_align_fused(T, E, k, n_loc)) {
     hipError_t e = launch_router_topk(logits, T, E, k, renorm, ids, w, s);
     if (e != hipSuccess) return e;
-    return launch_align(ids, T, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, s);
+    return launch_align(ids, T, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, hist, s);
   }
 #define EIMOE_RA(L, V) \
   return launch_route_align_lv<L, V>(logits, T, E, k, renorm, e_lo, n_loc, ids, w, counts, offsets, sorted_flat, \

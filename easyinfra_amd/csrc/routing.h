@@ -181,39 +181,18 @@ __device__ __forceinline__ uint64_t match_mask(int e, int nbits, uint64_t valid)
 
 constexpr int align_lds_ints(int n_loc) { return kAlignWaves * n_loc + 2 * n_loc + 1; }
 
-// Counting sort of N = T*k flat ids by local expert, in one workgroup of kAlignThreads
-// threads; lds holds align_lds_ints(n_loc) ints.  ids may point to global memory or LDS.
-// Each wave takes its ids in batches of kAlignBatch rows of 64; ROLLED walks a batch's
-// rows in a loop (small code: measured faster for a few hundred ids, where the kernel is
-// latency-bound), otherwise the rows are unrolled so their ballot chains overlap (faster
-// from a few thousand ids: 24 vs 36 us at 16384).
+// Per-wave histogram of the local experts of flat ids [beg, end) into hist_w[n_loc]
+// (one wave; the leader of each group of equal ids adds its group's size).  ROLLED walks a
+// batch's rows in a loop (small code: measured faster for a few hundred ids, where the
+// kernel is latency-bound), otherwise the rows are unrolled so their ballot chains overlap.
 template <bool ROLLED>
-__device__ __forceinline__ void align_rows(const int32_t* __restrict__ ids, int N, int k, int e_lo, int n_loc,
-                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                           int32_t* __restrict__ sorted_flat, int32_t* __restrict__ sorted_tok,
-                                           int32_t* __restrict__ pos, int* lds) {
-  int* hist = lds;                              // [kAlignWaves][n_loc]
-  int* tot = lds + kAlignWaves * n_loc;         // [n_loc]
-  int* offs = tot + n_loc;                      // [n_loc + 1]
-  const int tid = threadIdx.x;
-  const int w = tid >> 6;
-  const int lane = tid & 63;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-
-  int chunk = (N + kAlignWaves - 1) / kAlignWaves;
-  chunk = (chunk + 63) & ~63;
-  const int beg = w * chunk;
-  const int end = min(N, beg + chunk);
-  const int nbits = n_loc > 1 ? 32 - __clz(n_loc - 1) : 0;
-
-  for (int i = tid; i < kAlignWaves * n_loc; i += kAlignThreads) hist[i] = 0;
-  __syncthreads();
-
-  // pass 1: per-wave histogram
+__device__ __forceinline__ void count_slice(const int32_t* __restrict__ ids, int beg, int end, int e_lo, int n_loc,
+                                            int nbits, int* hist_w) {
+  const int lane = threadIdx.x & 63;
   auto count_row = [&](int e) {
     const uint64_t valid = __ballot(e >= 0);
     const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
-    if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1) hist[w * n_loc + e] += __popcll(m);
+    if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1) hist_w[e] += __popcll(m);
   };
   for (int i0 = beg; i0 < end; i0 += 64 * kAlignBatch) {
     int eb[kAlignBatch];
@@ -226,52 +205,24 @@ __device__ __forceinline__ void align_rows(const int32_t* __restrict__ ids, int 
       for (int r = 0; r < kAlignBatch; ++r) count_row(eb[r]);
     }
   }
-  __syncthreads();
+}
 
-  // per expert: exclusive prefix over waves and total count
-  for (int e = tid; e < n_loc; e += kAlignThreads) {
-    int run = 0;
-    for (int ww = 0; ww < kAlignWaves; ++ww) {
-      const int c = hist[ww * n_loc + e];
-      hist[ww * n_loc + e] = run;
-      run += c;
-    }
-    tot[e] = run;
-    counts[e] = run;
-  }
-  __syncthreads();
-
-  // exclusive scan over experts (wave 0)
-  if (w == 0) {
-    const int per = (n_loc + 63) / 64;
-    const int b0 = lane * per;
-    int s = 0;
-    for (int j = 0; j < per; ++j)
-      if (b0 + j < n_loc) s += tot[b0 + j];
-    const int incl = wave_incl_scan(s);
-    int run = incl - s;
-    for (int j = 0; j < per; ++j) {
-      if (b0 + j < n_loc) {
-        offs[b0 + j] = run;
-        run += tot[b0 + j];
-      }
-    }
-    if (lane == 63) offs[n_loc] = incl;
-  }
-  __syncthreads();
-  for (int i = tid; i <= n_loc; i += kAlignThreads) offsets[i] = offs[i];
-  for (int i = tid; i < kAlignWaves * n_loc; i += kAlignThreads) hist[i] += offs[i % n_loc];
-  __syncthreads();
-
-  // pass 2: stable placement.  All lanes read their cursor before the group leader
-  // advances it; one wave's LDS operations execute in program order.
+// Stable placement of flat ids [beg, end) (one wave): an id's slot is its expert's cursor
+// cur_w[e] plus its rank among equal ids below it in the row; the group leader advances
+// the cursor after every lane has read it (one wave's LDS operations run in program order).
+template <bool ROLLED>
+__device__ __forceinline__ void place_slice(const int32_t* __restrict__ ids, int beg, int end, int k, int e_lo,
+                                            int n_loc, int nbits, int* cur_w, int32_t* __restrict__ sorted_flat,
+                                            int32_t* __restrict__ sorted_tok, int32_t* __restrict__ pos) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   auto place_row = [&](int i, int e) {
     const uint64_t valid = __ballot(e >= 0);
     const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
     int p = -1;
-    if (e >= 0) p = hist[w * n_loc + e] + __popcll(m & lt_mask);
+    if (e >= 0) p = cur_w[e] + __popcll(m & lt_mask);
     __builtin_amdgcn_wave_barrier();
-    if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1) hist[w * n_loc + e] += __popcll(m);
+    if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1) cur_w[e] += __popcll(m);
     if (i < end) {
       pos[i] = p;
       if (p >= 0) {
@@ -291,6 +242,74 @@ __device__ __forceinline__ void align_rows(const int32_t* __restrict__ ids, int 
       for (int r = 0; r < kAlignBatch; ++r) place_row(i0 + r * 64 + lane, eb[r]);
     }
   }
+}
+
+// Exclusive scan of tot[0, n) into offs[0, n] by wave 0 (offs[n] = total).
+__device__ __forceinline__ void scan_experts(const int* tot, int n, int* offs) {
+  const int lane = threadIdx.x & 63;
+  if ((threadIdx.x >> 6) == 0) {
+    const int per = (n + 63) / 64;
+    const int b0 = lane * per;
+    int s = 0;
+    for (int j = 0; j < per; ++j)
+      if (b0 + j < n) s += tot[b0 + j];
+    const int incl = wave_incl_scan(s);
+    int run = incl - s;
+    for (int j = 0; j < per; ++j) {
+      if (b0 + j < n) {
+        offs[b0 + j] = run;
+        run += tot[b0 + j];
+      }
+    }
+    if (lane == 63) offs[n] = incl;
+  }
+}
+
+// Counting sort of N = T*k flat ids by local expert, in one workgroup of kAlignThreads
+// threads; lds holds align_lds_ints(n_loc) ints.  ids may point to global memory or LDS.
+// Each wave takes a contiguous slice of the ids in batches of kAlignBatch rows of 64
+// (ROLLED: see count_slice; unrolled measured faster from a few thousand ids: 24 vs 36 us
+// at 16384).
+template <bool ROLLED>
+__device__ __forceinline__ void align_rows(const int32_t* __restrict__ ids, int N, int k, int e_lo, int n_loc,
+                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                           int32_t* __restrict__ sorted_flat, int32_t* __restrict__ sorted_tok,
+                                           int32_t* __restrict__ pos, int* lds) {
+  int* hist = lds;                              // [kAlignWaves][n_loc]
+  int* tot = lds + kAlignWaves * n_loc;         // [n_loc]
+  int* offs = tot + n_loc;                      // [n_loc + 1]
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+
+  int chunk = (N + kAlignWaves - 1) / kAlignWaves;
+  chunk = (chunk + 63) & ~63;
+  const int beg = w * chunk;
+  const int end = min(N, beg + chunk);
+  const int nbits = n_loc > 1 ? 32 - __clz(n_loc - 1) : 0;
+
+  for (int i = tid; i < kAlignWaves * n_loc; i += kAlignThreads) hist[i] = 0;
+  __syncthreads();
+  count_slice<ROLLED>(ids, beg, end, e_lo, n_loc, nbits, hist + w * n_loc);   // pass 1: per-wave histogram
+  __syncthreads();
+
+  // per expert: exclusive prefix over waves and total count
+  for (int e = tid; e < n_loc; e += kAlignThreads) {
+    int run = 0;
+    for (int ww = 0; ww < kAlignWaves; ++ww) {
+      const int c = hist[ww * n_loc + e];
+      hist[ww * n_loc + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+    counts[e] = run;
+  }
+  __syncthreads();
+  scan_experts(tot, n_loc, offs);
+  __syncthreads();
+  for (int i = tid; i <= n_loc; i += kAlignThreads) offsets[i] = offs[i];
+  for (int i = tid; i < kAlignWaves * n_loc; i += kAlignThreads) hist[i] += offs[i % n_loc];
+  __syncthreads();
+  place_slice<ROLLED>(ids, beg, end, k, e_lo, n_loc, nbits, hist + w * n_loc, sorted_flat, sorted_tok, pos);   // pass 2
 }
 
 }  // namespace eimoe

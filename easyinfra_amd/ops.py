@@ -141,12 +141,16 @@ def eplb_map(topk_ids: torch.Tensor, log2phy: torch.Tensor, replica_count: torch
     return out
 
 
-def align(topk_ids: torch.Tensor, n_local: int, e_lo: int = 0) -> dict:
-    """Counts/offsets/stable permutation (blocks/moe/base.py:343-364, moe_all2all.py:346-348)."""
+def align(topk_ids: torch.Tensor, n_local: int, e_lo: int = 0, one_workgroup: bool = False) -> dict:
+    """Counts/offsets/stable permutation (blocks/moe/base.py:343-364, moe_all2all.py:346-348).
+    Large batches sort over many workgroups (a small workspace); ``one_workgroup`` forces the
+    single-workgroup kernel (the same result)."""
     _req(topk_ids, "topk_ids", torch.int32, 2)
     T, k = topk_ids.shape
     dev = topk_ids.device
     A = T * k
+    need = 0 if one_workgroup else int(_lib.lib().eimoe_align_workspace_bytes(T, k, n_local))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
     out = {
         "counts": torch.empty(n_local, dtype=torch.int32, device=dev),
         "offsets": torch.empty(n_local + 1, dtype=torch.int32, device=dev),
@@ -156,7 +160,7 @@ def align(topk_ids: torch.Tensor, n_local: int, e_lo: int = 0) -> dict:
     }
     call("eimoe_align", topk_ids.data_ptr(), T, k, e_lo, n_local, out["counts"].data_ptr(),
          out["offsets"].data_ptr(), out["sorted_flat"].data_ptr(), out["sorted_tok"].data_ptr(),
-         out["pos"].data_ptr(), _stream(topk_ids))
+         out["pos"].data_ptr(), _ptr(ws), need, _stream(topk_ids))
     return out
 
 

@@ -101,9 +101,13 @@ int eimoe_eplb_map(const int32_t* topk_ids, int T, int k, const int32_t* log2phy
  * Outputs: counts[n_local], offsets[n_local+1] (offsets[n_local] = rows kept),
  * sorted_flat[T*k] (flat index t*k+slot per row), sorted_tok[T*k] (t per row),
  * pos[T*k] (row of each flat index, -1 if not local).  Rows beyond offsets[n_local] are untouched.
- * 1 <= n_local <= EIMOE_MAX_EXPERTS. */
+ * 1 <= n_local <= EIMOE_MAX_EXPERTS.  workspace (eimoe_align_workspace_bytes(T, k, n_local) bytes;
+ * may be NULL) lets large batches (from 4096 routed pairs) spread the sort over many workgroups
+ * in two launches; without it one workgroup sorts.  Same result either way. */
+size_t eimoe_align_workspace_bytes(int T, int k, int n_local);
 int eimoe_align(const int32_t* topk_ids, int T, int k, int e_lo, int n_local, int32_t* counts, int32_t* offsets,
-                int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* stream);
+                int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, void* workspace, size_t workspace_bytes,
+                void* stream);
 
 /* Router then align in one call: the outputs of eimoe_router_topk followed by eimoe_align on
  * its ids, same arguments, same results bit for bit.  Small batches run both phases in one

@@ -50,10 +50,15 @@ def test_router_validation():
 
 
 def test_align_validation():
-    assert _rc("eimoe_align", None, 4, 2, 0, 0, None, None, None, None, None, None) == _lib.ERR_SHAPE
-    assert _rc("eimoe_align", None, 4, 2, -1, 8, None, None, None, None, None, None) == _lib.ERR_SHAPE
-    assert _rc("eimoe_align", None, 4, 40, 0, 8, None, None, None, None, None, None) == _lib.ERR_SHAPE
-    assert _rc("eimoe_align", None, 4, 2, 0, 8, None, None, None, None, None, None) == _lib.ERR_NULL
+    assert _rc("eimoe_align", None, 4, 2, 0, 0, None, None, None, None, None, None, 0, None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_align", None, 4, 2, -1, 8, None, None, None, None, None, None, 0, None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_align", None, 4, 40, 0, 8, None, None, None, None, None, None, 0, None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_align", None, 4, 2, 0, 8, None, None, None, None, None, None, 0, None) == _lib.ERR_NULL
+    # the many-workgroup sort's chunk counts: none below 4096 routed pairs, one row of n_local per ~1024 pairs
+    ws = _lib.lib().eimoe_align_workspace_bytes
+    assert ws(1000, 4, 64) == 0
+    assert ws(8192, 2, 8) == 16 * 8 * 4
+    assert ws(16384, 8, 512) == 32 * 512 * 4                  # at most 16384 matrix cells
 
 
 def test_route_align_validation():

@@ -173,6 +173,34 @@ def test_align_bit_exact(dev, T, k, E, e_lo, n_loc, skew):
     assert np.array_equal(cpu(got["pos"]).numpy(), ref["pos"])
 
 
+# From 4096 routed pairs the sort runs over many workgroups (chunk counts, then placement);
+# it must equal the one-workgroup kernel and the oracle bit for bit, including chunks that
+# end mid-row, every id on one expert, window filtering and the largest expert count.
+@pytest.mark.parametrize("T,k,E,e_lo,n_loc,mode", [
+    (4096, 1, 8, 0, 8, "uniform"), (4097, 1, 16, 0, 16, "uniform"), (2731, 3, 64, 16, 32, "uniform"),
+    (3000, 8, 128, 0, 32, "one"), (16384, 8, 512, 0, 512, "uniform"), (65536, 2, 8, 0, 8, "skew"),
+    (5000, 6, 64, 0, 64, "skew"),
+])
+def test_align_many_workgroups_bit_exact(dev, T, k, E, e_lo, n_loc, mode):
+    g = torch.Generator().manual_seed(T + k)
+    if mode == "one":
+        ids = torch.full((T, k), e_lo + 3, dtype=torch.int32)
+        ids[:, 1:] = torch.arange(1, k, dtype=torch.int32) + E // 2   # the other slots: distinct, off-window
+    else:
+        wts = (1.0 / torch.arange(1, E + 1, dtype=torch.float32) ** 1.2) if mode == "skew" else None
+        ids = _distinct_ids(T, E, k, g, wts)
+    many = ops.align(ids.to(dev), n_loc, e_lo)
+    one = ops.align(ids.to(dev), n_loc, e_lo, one_workgroup=True)
+    ref = oracle.align(ids.numpy(), n_loc, e_lo)
+    A = int(ref["offsets"][-1])
+    for got in (many, one):
+        assert np.array_equal(cpu(got["counts"]).numpy(), ref["counts"])
+        assert np.array_equal(cpu(got["offsets"]).numpy(), ref["offsets"])
+        assert np.array_equal(cpu(got["sorted_flat"])[:A].numpy(), ref["sorted_flat"])
+        assert np.array_equal(cpu(got["sorted_tok"])[:A].numpy(), ref["sorted_tok"])
+        assert np.array_equal(cpu(got["pos"]).numpy(), ref["pos"])
+
+
 def test_align_all_to_one_expert_and_repeats(dev):
     ids = torch.full((300, 4), 3, dtype=torch.int32)
     ids[::7, 1] = 0
