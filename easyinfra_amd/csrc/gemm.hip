@@ -802,7 +802,7 @@ int gemm_out_cols_per_tile(int tile, int epi) {
 //    us skewed, 580 vs 657 uniform against 128x128); the down projection (short K) wants
 //    more, smaller tiles: 128x128 below ~384 expected rows per segment (Qwen3 2048 tokens:
 //    46 vs 62 us), 32x128 below ~96.
-int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
+int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
   const int S = p.S > 0 ? p.S : 1;
   const double avg_bound = static_cast<double>(p.max_rows) / S;
   const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) / S;
@@ -810,7 +810,10 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
   const bool silu = epi == kEpiSiluBF16;
   int t;
   if (expert_bytes >= 32.0 * 1024 * 1024) {
-    if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 128 ? kTileM : kTileL;
+    // W8A8 gate/up streams its weights below ~48 rows per expert (Mixtral-8x7B, 8-64 rows
+    // per expert: 170-190 us streamed against 208-211 us on 32x128 tiles; equal at 32)
+    if (b_fp8 && a_fp8 && silu) t = avg < 48 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    else if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 128 ? kTileM : kTileL;
     else if (silu) t = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
     else t = avg < 8 ? kTileXS : avg < 128 ? kTileM : kTileL;
   } else if (silu) {
@@ -835,7 +838,7 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
   // activations (W8A16) stay on the LDS-tiled kernels.
   const bool stream_ok = (b_fp8 == a_fp8) && stream_gemm_supported(p, epi, a_fp8);
   if (tile == kTileAuto) {
-    tile = gemm_pick_tile(p, epi, b_fp8);
+    tile = gemm_pick_tile(p, epi, b_fp8, a_fp8);
     // a few rows per segment: stream the weights instead of tiling them through LDS
     if (tile == kTileXS && stream_ok) tile = kTileStream;
   }
