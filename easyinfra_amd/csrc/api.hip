@@ -104,7 +104,7 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
   q.K = I;
   q.k_split = 1;
   q.nb_rows = H;
-  const int tile = gemm_pick_tile(q, kEpiStoreF32, w8a8, w8a8);
+  const int tile = gemm_pick_tile(q, kEpiStoreF32, w8a8);
   if (tile == kTileXS) {
     // Few rows per segment: the weight-streaming kernel runs one workgroup per (segment,
     // column group, 32-row chunk, split).  Split until there are about 6 workgroups per CU

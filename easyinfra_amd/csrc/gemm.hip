@@ -802,7 +802,7 @@ int gemm_out_cols_per_tile(int tile, int epi) {
 //    us skewed, 580 vs 657 uniform against 128x128); the down projection (short K) wants
 //    more, smaller tiles: 128x128 below ~384 expected rows per segment (Qwen3 2048 tokens:
 //    46 vs 62 us), 32x128 below ~96.
-int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
+int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
   const int S = p.S > 0 ? p.S : 1;
   const double avg_bound = static_cast<double>(p.max_rows) / S;
   const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) / S;
@@ -837,7 +837,7 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
   // activations (W8A16) stay on the LDS-tiled kernels.
   const bool stream_ok = (b_fp8 == a_fp8) && stream_gemm_supported(p, epi, a_fp8);
   if (tile == kTileAuto) {
-    tile = gemm_pick_tile(p, epi, b_fp8, a_fp8);
+    tile = gemm_pick_tile(p, epi, b_fp8);
     // a few rows per segment: stream the weights instead of tiling them through LDS
     if (tile == kTileXS && stream_ok) tile = kTileStream;
   }

@@ -101,7 +101,7 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
                                hipStream_t s);
 // Tile for a launch: from the expected rows per segment, the output width and the bytes of
 // one expert's weights (rows_hint/max_rows, p.S, p.N, p.K * p.k_split, nb_rows).
-int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8);
+int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8);
 // Weight-streaming kernel (stream.hip) for segments of a few rows: bf16 x bf16, or
 // e4m3 x e4m3 (fp8 = true, W8A8 with p.a_scale / p.b_scale).
 bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8);
