@@ -750,7 +750,10 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
 
 // bf16 256x256 tiles: the ping-pong kernel (3-4 % faster than the lock-step 8-wave kernel on
 // the Mixtral-8x7B prefill GEMMs, bit-identical results).
-template <int EPI>
+// Tile grouping depth 4.  16 measured 3 % faster on the bare Mixtral prefill GEMMs (gate/up
+// 3.16 vs 3.25 ms) but not on whole layers (Mixtral 8192 tokens 4.94-4.98 vs 4.92-4.95 ms;
+// DeepSeek-V2-Lite and Qwen3 within noise), so the layer's figure decides.
+template <int EPI, int GMX = 4>
 static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
   constexpr int OUT_BN = (EPI == kEpiSiluBF16) ? 128 : 256;
   const int n_tiles = p.N / OUT_BN;
@@ -759,7 +762,7 @@ static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
   long long grid = (total + kNumXcd - 1) / kNumXcd * kNumXcd;
   if (grid < kNumXcd) grid = kNumXcd;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((grouped_gemm_pp_kernel<EPI, 4>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, s, p);
+  hipLaunchKernelGGL((grouped_gemm_pp_kernel<EPI, GMX>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, s, p);
   return hipGetLastError();
 }
 
