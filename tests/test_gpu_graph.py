@@ -1,4 +1,4 @@
-"""The fused layer under HIP graph capture.
+"""The fused layer and the MoE prologue under HIP graph capture.
 
 A serving loop captures the layer once and replays it with new contents in the same
 input buffers.  Each replay must equal an eager call on the same inputs bit for bit (the
@@ -75,3 +75,38 @@ def test_fused_moe_graph_replays_match_eager(dev, name, T, w8a8):
         again = ops.fused_moe(xs[2 - j // 2], lgs[2 - j // 2], k, wgu, wd, **kw)
         torch.cuda.synchronize()
         assert torch.equal(again, eager[2 - j // 2])
+
+
+# The prologue's router GEMM path (K-split planes and their sum, the segment offsets written
+# by the norm kernel) and its one-pass path, replayed with new inputs.
+@pytest.mark.parametrize("T,H,E,lbf16", [(512, 7168, 256, False), (300, 4096, 8, True)])
+def test_moe_prologue_graph_replays_match_eager(dev, T, H, E, lbf16):
+    g = torch.Generator().manual_seed(T + E)
+    hs = [(torch.randn(T, H, generator=g) * (1 + j)).to(torch.bfloat16).to(dev) for j in range(3)]
+    rs = [torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(3)]
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+    gw = (0.05 * torch.randn(E, H, generator=g)).to(torch.bfloat16).to(dev)
+    eager = [ops.moe_prologue(h, r, w, 1e-6, gw, lbf16) for h, r in zip(hs, rs)]
+    torch.cuda.synchronize()
+    h_s, r_s = hs[0].clone(), rs[0].clone()
+    need = ops.moe_prologue_workspace_bytes(T, H, E)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.moe_prologue(h_s, r_s, w, 1e-6, gw, lbf16, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_s = ops.moe_prologue(h_s, r_s, w, 1e-6, gw, lbf16, workspace=ws)
+    for j in (2, 0, 1):
+        h_s.copy_(hs[j])
+        r_s.copy_(rs[j])
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(out_s, eager[j]):
+            assert torch.equal(got, want), f"replay with inputs {j} differs from the eager call"
+        again = ops.moe_prologue(hs[2 - j], rs[2 - j], w, 1e-6, gw, lbf16)
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(again, eager[2 - j]))
