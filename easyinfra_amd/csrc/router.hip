@@ -257,6 +257,10 @@ __global__ __launch_bounds__(kAlignThreads) void route_align_kernel(
   int* s_ids = lds + align_lds_ints(n_loc);   // [T*k] after the align's histogram
   route_rows<LPT, VPL, KMAX, true>(logits, T, E, k, renorm, ids, wts, s_ids, threadIdx.x >> 6, kAlignWaves);
   __syncthreads();
+  if (T * k <= 64) {   // a decode step's few ids: one wave sorts them without further barriers
+    if (threadIdx.x < 64) align_tiny(s_ids, T * k, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, lds);
+    return;
+  }
   align_rows<true>(s_ids, T * k, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, lds);
 }
 

@@ -265,6 +265,44 @@ __device__ __forceinline__ void scan_experts(const int* tot, int n, int* offs) {
   }
 }
 
+// The same sort for at most 64 flat ids, by one wave with no workgroup barrier: lane i
+// holds id i, the match mask of its expert gives its group's size (written by the group's
+// lowest lane) and its rank, and a wave scan over the experts gives the offsets.
+// lds holds 2*n_loc + 1 ints.  Same outputs as align_rows.
+__device__ __forceinline__ void align_tiny(const int32_t* __restrict__ ids, int N, int k, int e_lo, int n_loc,
+                                           int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                           int32_t* __restrict__ sorted_flat, int32_t* __restrict__ sorted_tok,
+                                           int32_t* __restrict__ pos, int* lds) {
+  int* cnt = lds;            // [n_loc]
+  int* offs = lds + n_loc;   // [n_loc + 1]
+  const int lane = threadIdx.x & 63;
+  const int nbits = n_loc > 1 ? 32 - __clz(n_loc - 1) : 0;
+  for (int e = lane; e < n_loc; e += 64) cnt[e] = 0;
+  __builtin_amdgcn_wave_barrier();
+  int e = -1;
+  if (lane < N) {
+    const int g = ids[lane] - e_lo;
+    e = (g >= 0 && g < n_loc) ? g : -1;
+  }
+  const uint64_t valid = __ballot(e >= 0);
+  const uint64_t m = match_mask(e < 0 ? 0 : e, nbits, valid);
+  if (e >= 0 && lane == __ffsll(static_cast<unsigned long long>(m)) - 1) cnt[e] = __popcll(m);
+  __builtin_amdgcn_wave_barrier();
+  scan_experts(cnt, n_loc, offs);
+  __builtin_amdgcn_wave_barrier();
+  for (int x = lane; x < n_loc; x += 64) counts[x] = cnt[x];
+  for (int x = lane; x <= n_loc; x += 64) offsets[x] = offs[x];
+  if (lane < N) {
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int p = e >= 0 ? offs[e] + __popcll(m & lt_mask) : -1;
+    pos[lane] = p;
+    if (p >= 0) {
+      sorted_flat[p] = lane;
+      sorted_tok[p] = lane / k;
+    }
+  }
+}
+
 // Counting sort of N = T*k flat ids by local expert, in one workgroup of kAlignThreads
 // threads; lds holds align_lds_ints(n_loc) ints.  ids may point to global memory or LDS.
 // Each wave takes a contiguous slice of the ids in batches of kAlignBatch rows of 64

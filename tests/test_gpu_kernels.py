@@ -228,6 +228,9 @@ def test_align_out_of_window_ids_dropped(dev):
     (1, 8, 2, 0, 8, True), (64, 8, 2, 0, 8, True), (256, 8, 2, 0, 8, True), (257, 8, 2, 0, 8, True),
     (32, 128, 8, 0, 32, True), (128, 128, 8, 32, 32, True), (129, 128, 8, 0, 32, True), (60, 64, 6, 0, 64, False),
     (7, 256, 16, 50, 100, True), (64, 200, 20, 0, 200, False), (3, 300, 4, 0, 300, True), (5, 16, 1, 3, 1, True),
+    # at most 64 routed pairs: the one-wave sort
+    (1, 128, 8, 0, 32, True), (8, 128, 8, 32, 32, True), (3, 256, 8, 0, 256, False), (5, 64, 6, 16, 16, True),
+    (32, 8, 2, 0, 8, True), (1, 8, 2, 6, 2, False), (4, 256, 16, 0, 256, True),
 ])
 def test_route_align_bit_exact(dev, T, E, k, e_lo, n_loc, renorm):
     g = torch.Generator().manual_seed(T * 31 + E)
