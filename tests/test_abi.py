@@ -181,3 +181,16 @@ def test_ops_refuse_cpu_tensors():
     from easyinfra_amd import ops
     with pytest.raises(ValueError):
         ops.router_topk(torch.zeros(4, 8), 2)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    # one GPU per box: the multi-GPU launch exits with a message instead of measuring
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
+    assert r.stdout.strip() == ""
