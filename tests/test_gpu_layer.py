@@ -164,3 +164,29 @@ def test_layer_real_shape(dev, name, T):
     assert rel <= 1e-2
     # Max-abs 2e-2 at the stated magnitude; fp32 output, bf16 intermediate h.
     assert mx <= 2e-2 * max(1.0, float(ref.abs().max()) / 4.0)
+
+
+def test_block_prologue_then_v3_layer(dev):
+    """The MoE block as a caller chains it: prologue (residual add, RMSNorm, fp32 router GEMM)
+    then the layer with the DeepSeek-V3 gate and shared experts, against the oracle run on the
+    GPU's own normed rows and logits (the prologue's parity is tested on its own)."""
+    g = torch.Generator().manual_seed(11)
+    T, H, I, E, k, Is = 100, 256, 128, 64, 6, 256
+    hid = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    res = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ln = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    gate = (0.1 * torch.randn(E, H, generator=g)).to(torch.bfloat16)
+    bias = 0.1 * torch.randn(E, generator=g)
+    wgu = (0.05 * torch.randn(E, 2 * I, H, generator=g)).to(torch.bfloat16)
+    wd = (0.05 * torch.randn(E, H, I, generator=g)).to(torch.bfloat16)
+    sg = (0.05 * torch.randn(2 * Is, H, generator=g)).to(torch.bfloat16)
+    sd = (0.05 * torch.randn(H, Is, generator=g)).to(torch.bfloat16)
+    r = res.to(dev)
+    r, normed, logits = ops.moe_prologue(hid.to(dev), r, ln.to(dev), 1e-6, gate.to(dev), logits_bf16=False,
+                                         residual_out=r)
+    out = ops.fused_moe(normed, logits, k, wgu.to(dev), wd.to(dev), scoring_func="sigmoid", n_group=8,
+                        topk_group=4, e_score_correction_bias=bias.to(dev), routed_scaling_factor=2.5,
+                        shared_gate_up=sg.to(dev), shared_down=sd.to(dev), out_dtype=torch.float32)
+    ids, w = oracle.route_grouped_topk(cpu(logits), k, 8, 4, bias, True, 2.5)
+    ref = oracle.moe_forward(cpu(normed), cpu(logits), k, wgu, wd, True, sg, sd, routing=(ids, w))
+    assert oracle.rel_l2(cpu(out), ref) <= 1e-2
