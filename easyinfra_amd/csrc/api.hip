@@ -152,8 +152,10 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
 }
 
 struct FusedLayout {
-  size_t ids, w, counts, offsets, sorted_flat, sorted_tok, pos, hist, h, y, sh_off, sh_h, sh_y, xq, sx, hq, sh, total;
+  size_t ids, w, counts, offsets, sorted_flat, sorted_tok, pos, hist, h, h_lo, y, sh_off, sh_h, sh_h_lo, sh_y, xq, sx,
+      hq, sh, total;
   int k_split;
+  int h_terms;   // 2 with EIMOE_H_SPLIT: h stored as bf16 hi + lo, each projected into its own y planes
   int y_dtype;
   int rows_hint;
 };
@@ -169,7 +171,8 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   FusedLayout L{};
   const size_t A = static_cast<size_t>(T) * k;
   L.rows_hint = local_rows_hint(T, k, E, n_local);
-  L.y_dtype = ((flags & EIMOE_Y_F32) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
+  L.h_terms = (flags & EIMOE_H_SPLIT) ? 2 : 1;
+  L.y_dtype = ((flags & (EIMOE_Y_F32 | EIMOE_H_SPLIT)) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
   L.k_split = pick_down_split(static_cast<int>(A), L.rows_hint, n_local, H, I,
                               static_cast<int>(elem_size(L.y_dtype)), (flags & EIMOE_W8A8) != 0);
   size_t o = 0;
@@ -187,7 +190,8 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   L.pos = take(A * 4);
   L.hist = take(align_plan(static_cast<int>(A), n_local).hist_ints * 4);
   L.h = take(A * I * 2);
-  L.y = take(static_cast<size_t>(L.k_split) * A * H * elem_size(L.y_dtype));
+  if (L.h_terms == 2) L.h_lo = take(A * I * 2);
+  L.y = take(static_cast<size_t>(L.h_terms) * L.k_split * A * H * elem_size(L.y_dtype));
   if (flags & EIMOE_W8A8) {
     L.xq = take(static_cast<size_t>(T) * H);
     L.sx = take(static_cast<size_t>(T) * 4);
@@ -197,7 +201,8 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   if (Is > 0) {
     L.sh_off = take(2 * 4);
     L.sh_h = take(static_cast<size_t>(T) * Is * 2);
-    L.sh_y = take(static_cast<size_t>(T) * H * elem_size(L.y_dtype));
+    if (L.h_terms == 2) L.sh_h_lo = take(static_cast<size_t>(T) * Is * 2);
+    L.sh_y = take(static_cast<size_t>(L.h_terms) * T * H * elem_size(L.y_dtype));
   }
   L.total = o;
   return L;
@@ -212,8 +217,9 @@ __global__ void dense_segment_kernel(int32_t* off, int T) {
 
 int run_gate_up(const void* a, const int32_t* a_rows, long long a_nrows, int lda, const void* w, int w_dtype,
                 const float* w_scale, int H, int I, const int32_t* seg, int n_seg, int e_mod, int max_rows, void* h,
-                int tile, hipStream_t s, const float* a_scale = nullptr, int rows_hint = 0) {
+                int tile, hipStream_t s, const float* a_scale = nullptr, int rows_hint = 0, void* h_lo = nullptr) {
   GemmArgs p{};
+  p.c_lo = h_lo;
   p.rows_hint = rows_hint;
   p.a = a;
   p.a_rows = a_rows;
@@ -512,9 +518,14 @@ int eimoe_gemm_down_w8a8(const void* hq, const float* h_scale, int I, const void
                   tile, S(stream), h_scale);
 }
 
-int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* b, int b_dtype,
-                       const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
-                       int n_seg, int e_mod, int max_rows, void* c, int c_dtype, int tile, void* stream) {
+namespace {
+
+// The grouped GEMM of the op point, expert weights either packed (b, b_expert_stride elements
+// apart) or one [N, K] matrix per expert through a device table of b_ptrs.
+int grouped_gemm_impl(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* b,
+                      const void* const* b_ptrs, int b_dtype, const float* b_scale, long long b_expert_stride, int N,
+                      int K, const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows, void* c, int c_dtype,
+                      int tile, void* stream) {
   int rc = check_gemm_common(max_rows, n_seg, e_mod);
   if (rc) return rc;
   if (b_dtype != EIMOE_BF16 && b_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "b_dtype=%d", b_dtype);
@@ -533,7 +544,7 @@ int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int ld
   if ((rc = check_tile(tile, kEpiStoreF32, N))) return rc;
   if (max_rows == 0) return EIMOE_OK;
   REQUIRE_PTR(a);
-  REQUIRE_PTR(b);
+  if (!b && !b_ptrs) return fail(EIMOE_ERR_NULL, "b is NULL");
   REQUIRE_PTR(seg_offsets);
   REQUIRE_PTR(c);
   if (b_dtype == EIMOE_FP8) REQUIRE_PTR(b_scale);
@@ -542,6 +553,7 @@ int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int ld
   p.a_rows = a_rows;
   p.lda = lda;
   p.b = b;
+  p.b_ptrs = b_ptrs;
   p.b_estride = b_expert_stride;
   p.ldb = K;
   p.b_scale = b_scale;
@@ -561,6 +573,26 @@ int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int ld
                    "grouped_gemm");
 }
 
+}  // namespace
+
+int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* b, int b_dtype,
+                       const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
+                       int n_seg, int e_mod, int max_rows, void* c, int c_dtype, int tile, void* stream) {
+  return grouped_gemm_impl(a, a_rows, a_nrows, lda, b, nullptr, b_dtype, b_scale, b_expert_stride, N, K, seg_offsets,
+                           n_seg, e_mod, max_rows, c, c_dtype, tile, stream);
+}
+
+int eimoe_grouped_gemm_ptrs(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* const* b_ptrs,
+                            int n_b, int N, int K, const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows,
+                            void* c, int c_dtype, int tile, void* stream) {
+  if (n_b < 1) return fail(EIMOE_ERR_SHAPE, "n_b=%d < 1", n_b);
+  if (e_mod > n_b) return fail(EIMOE_ERR_SHAPE, "e_mod=%d > n_b=%d weight matrices", e_mod, n_b);
+  if (max_rows > 0) REQUIRE_PTR(b_ptrs);
+  return grouped_gemm_impl(a, a_rows, a_nrows, lda, nullptr, b_ptrs, EIMOE_BF16, nullptr,
+                           static_cast<long long>(N) * K, N, K, seg_offsets, n_seg, e_mod, max_rows, c, c_dtype, tile,
+                           stream);
+}
+
 int eimoe_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
                   const float* topk_weights, int T, int k, int H, const void* shared_y, int shared_dtype, void* out,
                   int out_dtype, void* stream) {
@@ -578,7 +610,7 @@ int eimoe_combine(const void* y, int y_dtype, int n_split, long long split_strid
   REQUIRE_PTR(topk_weights);
   REQUIRE_PTR(out);
   return hip_check(launch_combine(y, y_dtype, n_split, split_stride, pos, topk_weights, T, k, H, shared_y,
-                                  shared_dtype, out, out_dtype, S(stream)),
+                                  shared_dtype, 1, out, out_dtype, S(stream)),
                    "combine");
 }
 
@@ -654,6 +686,8 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   if (out_dtype != EIMOE_BF16 && out_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "out_dtype=%d", out_dtype);
   if (static_cast<long long>(T) * k > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "T*k overflows int32");
   if ((flags & EIMOE_W8A8) && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "EIMOE_W8A8 needs fp8 weights");
+  if ((flags & EIMOE_W8A8) && (flags & EIMOE_H_SPLIT))
+    return fail(EIMOE_ERR_DTYPE, "EIMOE_H_SPLIT keeps h in bf16 terms; W8A8 quantises it to fp8");
   if ((flags & EIMOE_W8A8) && (H % 128 || I % 128))
     return fail(EIMOE_ERR_ALIGN, "W8A8 needs H=%d and I=%d multiples of 128", H, I);
   {
@@ -723,11 +757,17 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
       int32_t* sh_off = static_cast<int32_t*>(at(L.sh_off));
       hipLaunchKernelGGL(dense_segment_kernel, dim3(1), dim3(64), 0, s2, sh_off, T);
       if ((rc = hip_check(hipGetLastError(), "shared offsets"))) return rc;
+      void* sh_lo = L.h_terms == 2 ? at(L.sh_h_lo) : nullptr;
       if ((rc = run_gate_up(x, nullptr, T, H, shared_gate_up, EIMOE_BF16, nullptr, H, shared_inter, sh_off, 1, 1, T,
-                            at(L.sh_h), EIMOE_TILE_AUTO, s2)))
+                            at(L.sh_h), EIMOE_TILE_AUTO, s2, nullptr, 0, sh_lo)))
         return rc;
-      return run_down(at(L.sh_h), shared_inter, shared_down, EIMOE_BF16, nullptr, H, sh_off, 1, 1, T, at(L.sh_y),
-                      L.y_dtype, 1, EIMOE_TILE_AUTO, s2);
+      if ((rc = run_down(at(L.sh_h), shared_inter, shared_down, EIMOE_BF16, nullptr, H, sh_off, 1, 1, T, at(L.sh_y),
+                         L.y_dtype, 1, EIMOE_TILE_AUTO, s2)))
+        return rc;
+      if (!sh_lo) return EIMOE_OK;
+      return run_down(sh_lo, shared_inter, shared_down, EIMOE_BF16, nullptr, H, sh_off, 1, 1, T,
+                      at(L.sh_y + static_cast<size_t>(T) * H * elem_size(L.y_dtype)), L.y_dtype, 1, EIMOE_TILE_AUTO,
+                      s2);
     };
     rc = shared();
     if (aux) {
@@ -770,11 +810,17 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
                          L.k_split, EIMOE_TILE_AUTO, s, sh, L.rows_hint)))
         return rc;
     } else {
+      void* h_lo = L.h_terms == 2 ? at(L.h_lo) : nullptr;
       if ((rc = run_gate_up(x, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
-                            A, at(L.h), EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
+                            A, at(L.h), EIMOE_TILE_AUTO, s, nullptr, L.rows_hint, h_lo)))
         return rc;
       if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y),
                          L.y_dtype, L.k_split, EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
+        return rc;
+      // the lo term into the planes after the hi term's (the combine sums them all)
+      if (h_lo && (rc = run_down(h_lo, I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A,
+                                 at(L.y + static_cast<size_t>(L.k_split) * A * H * elem_size(L.y_dtype)), L.y_dtype,
+                                 L.k_split, EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
         return rc;
     }
     return EIMOE_OK;
@@ -785,8 +831,8 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
     if (!rc) rc = rj;
   }
   if (rc) return rc;
-  return hip_check(launch_combine(at(L.y), L.y_dtype, L.k_split, static_cast<long long>(A) * H, pos, w, T, k, H, sh_y,
-                                  L.y_dtype, out, out_dtype, s),
+  return hip_check(launch_combine(at(L.y), L.y_dtype, L.h_terms * L.k_split, static_cast<long long>(A) * H, pos, w, T,
+                                  k, H, sh_y, L.y_dtype, L.h_terms, out, out_dtype, s),
                    "combine");
 }
 

@@ -260,7 +260,13 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
           }
           h[j] = silu_f32(g) * u;
         }
-        store_bf16<G::NI>(static_cast<uint16_t*>(p.c) + static_cast<long long>(row) * p.ldc + col0, h);
+        const long long off = static_cast<long long>(row) * p.ldc + col0;
+        store_bf16<G::NI>(static_cast<uint16_t*>(p.c) + off, h);
+        if (p.c_lo) {   // the residual of the bf16 rounding, itself in bf16
+#pragma unroll
+          for (int j = 0; j < G::NI; ++j) h[j] -= bf16_to_f32(f32_to_bf16(h[j]));
+          store_bf16<G::NI>(static_cast<uint16_t*>(p.c_lo) + off, h);
+        }
       } else {
         const int col0 = tc.n_tile * G::OUT_BN + wn * G::WN + lr * G::NI;
         float v[G::NI];
@@ -384,7 +390,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
     const long long src = p.a_rows ? static_cast<long long>(p.a_rows[gr]) : static_cast<long long>(gr);
     a_voff[i] = static_cast<uint32_t>(src * p.lda * 2 + (((lane & 7) ^ swz(row)) << 4));
   }
-  const uint16_t* b_base = static_cast<const uint16_t*>(p.b) + static_cast<long long>(tc.expert) * p.b_estride + k0;
+  const uint16_t* b_base = reinterpret_cast<const uint16_t*>(expert_weights(p, tc.expert, 2)) + k0;
   const BufRef rB{b_base, (p.b_estride - k0) * 2};
   uint32_t b_voff[B_PW];
 #pragma unroll
@@ -477,7 +483,7 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp_kernel(GemmArgs p) {
     const long long src = p.a_rows ? static_cast<long long>(p.a_rows[gr]) : static_cast<long long>(gr);
     a_voff[i] = static_cast<uint32_t>(src * p.lda * 2 + (((lane & 7) ^ swz(row)) << 4));
   }
-  const uint16_t* b_base = static_cast<const uint16_t*>(p.b) + static_cast<long long>(tc.expert) * p.b_estride + k0;
+  const uint16_t* b_base = reinterpret_cast<const uint16_t*>(expert_weights(p, tc.expert, 2)) + k0;
   const BufRef rB{b_base, (p.b_estride - k0) * 2};
   uint32_t b_voff[B_PW];
 #pragma unroll
@@ -604,7 +610,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8_kernel(GemmAr
     const long long src = p.a_rows ? static_cast<long long>(p.a_rows[gr]) : static_cast<long long>(gr);
     a_voff[i] = static_cast<uint32_t>(src * p.lda + (((lane & 7) ^ swz(row)) << 4));
   }
-  const uint8_t* b_base = static_cast<const uint8_t*>(p.b) + static_cast<long long>(tc.expert) * p.b_estride + k0;
+  const uint8_t* b_base = expert_weights(p, tc.expert, 1) + k0;
   const BufRef rB{b_base, p.b_estride - k0};
   uint32_t b_voff[B_PW];
 #pragma unroll
@@ -679,7 +685,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8w_kernel(GemmA
     const long long src = p.a_rows ? static_cast<long long>(p.a_rows[gr]) : static_cast<long long>(gr);
     a_voff[i] = static_cast<uint32_t>(src * p.lda * 2 + (((lane & 7) ^ swz(row)) << 4));
   }
-  const uint8_t* b_base = static_cast<const uint8_t*>(p.b) + static_cast<long long>(tc.expert) * p.b_estride + k0;
+  const uint8_t* b_base = expert_weights(p, tc.expert, 1) + k0;
   const BufRef rB{b_base, p.b_estride - k0};
   uint32_t b_voff[B_LD];
   int b_R[B_LD], b_c[B_LD];

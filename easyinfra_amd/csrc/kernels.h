@@ -18,6 +18,8 @@ struct GemmArgs {
   long long lda;
   const void* b;             // bf16 or fp8-e4m3 [E][N_b][K]
   long long b_estride;       // elements between experts
+  const void* const* b_ptrs; // optional: expert e's [N_b][K] weights at b_ptrs[e] (b, b_estride unused
+                             // for addressing; b_estride still bounds one expert's elements)
   long long ldb;
   const float* b_scale;      // fp8: per-output-channel scale [E][N_b]; null for bf16
   int nb_rows;               // N_b, rows per expert in b (scale indexing)
@@ -28,6 +30,7 @@ struct GemmArgs {
   int S;
   int e_mod;
   void* c;
+  void* c_lo;                // SiLU epilogue: also store bf16(h - bf16(h)) here (same layout as c); may be null
   long long ldc;
   long long c_split_stride;  // elements between split-K partial outputs
   int k_split;
@@ -92,9 +95,10 @@ hipError_t launch_moe_prologue(const void* hidden, const void* residual, const v
 
 hipError_t launch_gather_rows(const void* x, int row_bytes, const int32_t* rows, const int32_t* num_rows,
                               int max_rows, void* xs, hipStream_t s);
+// shared_n: planes of shared_y, T*H elements apart, summed (1 for a single plane).
 hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
-                          const float* w, int T, int k, int H, const void* shared_y, int shared_dtype, void* out,
-                          int out_dtype, hipStream_t s);
+                          const float* w, int T, int k, int H, const void* shared_y, int shared_dtype, int shared_n,
+                          void* out, int out_dtype, hipStream_t s);
 // epi: Epilogue; b_fp8: B is e4m3; max_rows bounds the grid; tile: TileCfg.
 // a_fp8: A and B are both fp8-e4m3 (W8A8 on the fp8 MFMA); b_fp8 alone: W8A16.
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
@@ -108,6 +112,12 @@ bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8);
 int stream_out_cols(int N, int epi, bool fp8);   // widest output columns per streaming task (0: unsupported)
 hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s);
 int gemm_out_cols_per_tile(int tile, int epi);
+
+// Base of expert e's weights: the pointer table when given, else b + e * b_estride elements.
+__device__ __forceinline__ const uint8_t* expert_weights(const GemmArgs& p, int e, int elem_bytes) {
+  return p.b_ptrs ? static_cast<const uint8_t*>(p.b_ptrs[e])
+                  : static_cast<const uint8_t*>(p.b) + static_cast<long long>(e) * p.b_estride * elem_bytes;
+}
 hipError_t launch_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, uint8_t* q, float* scale,
                                     hipStream_t s);
 

@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
                                                       long long split_stride, const int32_t* __restrict__ pos,
                                                       const float* __restrict__ w, int T, int k, int H,
                                                       const void* __restrict__ shared_y, int shared_dtype,
-                                                      void* __restrict__ out, int out_dtype) {
+                                                      int shared_n, void* __restrict__ out, int out_dtype) {
   const int cpr = H / 8;
   const long long total = static_cast<long long>(T) * cpr;
   for (long long i = blockIdx.x * 256ll + threadIdx.x; i < total; i += static_cast<long long>(gridDim.x) * 256) {
@@ -107,24 +107,31 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
       for (int q = 0; q < 8; ++q) acc[q] += wj * ys[q];
     }
     if (shared_y) {
-      float v[8];
-      load8(shared_y, shared_dtype, static_cast<long long>(t) * H + h, v);
+      float ys[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) acc[q] += v[q];
+      for (int q = 0; q < 8; ++q) ys[q] = 0.f;
+      for (int s = 0; s < shared_n; ++s) {
+        float v[8];
+        load8(shared_y, shared_dtype, (static_cast<long long>(s) * T + t) * H + h, v);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ys[q] += v[q];
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] += ys[q];
     }
     store8(out, out_dtype, static_cast<long long>(t) * H + h, acc);
   }
 }
 
 hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
-                          const float* w, int T, int k, int H, const void* shared_y, int shared_dtype, void* out,
-                          int out_dtype, hipStream_t s) {
+                          const float* w, int T, int k, int H, const void* shared_y, int shared_dtype, int shared_n,
+                          void* out, int out_dtype, hipStream_t s) {
   const long long total = static_cast<long long>(T) * (H / 8);
   long long blocks = (total + 255) / 256;
   if (blocks > 16384) blocks = 16384;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, y, y_dtype, n_split,
-                     split_stride, pos, w, T, k, H, shared_y, shared_dtype, out, out_dtype);
+                     split_stride, pos, w, T, k, H, shared_y, shared_dtype, shared_n, out, out_dtype);
   return hipGetLastError();
 }
 

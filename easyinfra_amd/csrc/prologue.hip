@@ -4,9 +4,9 @@
 //   MoeAll2AllBlock.all2all_chunk_routing_compute (generation/blocks/moe/moe_all2all.py:329-336):
 //     residual = _add_to_residual(residual, hidden_states)   (generation/utils/compute_utils.py:14)
 //     normed   = post_attention_layernorm(residual)
-//   _rmsnorm (generation/modules/norms/base_rmsnorm.py:6-12):
+//   _rmsnorm (generation/modules/rmsnorm/base_rmsnorm.py:6-12):
 //     t = r.float(); t = t * rsqrt(mean(t^2) + eps); normed = weight * t.to(bf16)
-//   the router gate, F.linear(normed, gate_w) (modules/linears/base_linear.py:28-36; in bf16 for
+//   the router gate, F.linear(normed, gate_w) (generation/modules/linear/base_linear.py:28-36; in bf16 for
 //   the Qwen3 / Mixtral gates, whose logits are therefore rounded to bf16) or
 //   F.linear(normed.float(), gate_w.float()) (DeepseekV3MoEGate, models/deepseek_v3/
 //   modeling_deepseek_v3.py:155-157; fp32 logits).

@@ -180,8 +180,7 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   const __amdgpu_buffer_rsrc_t ra =
       make_rsrc(static_cast<const uint8_t*>(p.a) + k0 * EB, (p.a_rows_cap * p.lda - k0) * EB);
   const __amdgpu_buffer_rsrc_t rb =
-      make_rsrc(static_cast<const uint8_t*>(p.b) + (static_cast<long long>(expert) * p.b_estride + k0) * EB,
-                (p.b_estride - k0) * EB);
+      make_rsrc(expert_weights(p, expert, EB) + k0 * EB, (p.b_estride - k0) * EB);
   uint32_t a_voff[MBLK], b_voff[NFRAG];
 #pragma unroll
   for (int m = 0; m < MBLK; ++m) {
@@ -274,8 +273,11 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
             g *= sc[wrow[f]];
             u *= sc[wrow[G + f]];
           }
-          static_cast<uint16_t*>(p.c)[static_cast<long long>(row) * p.ldc + col0 + f * 16 + lr] =
-              f32_to_bf16(silu_f32(g) * u);
+          const float h = silu_f32(g) * u;
+          const uint16_t hb = f32_to_bf16(h);
+          const long long off = static_cast<long long>(row) * p.ldc + col0 + f * 16 + lr;
+          static_cast<uint16_t*>(p.c)[off] = hb;
+          if (p.c_lo) static_cast<uint16_t*>(p.c_lo)[off] = f32_to_bf16(h - bf16_to_f32(hb));
         }
       } else {
 #pragma unroll

@@ -43,6 +43,19 @@ def _req(t: torch.Tensor, name: str, dtype=None, dim=None):
         raise ValueError(f"{name} must be {dim}-D, got {tuple(t.shape)}")
 
 
+def _req_shape(t: torch.Tensor, name: str, shape: Tuple[int, ...], dtype=torch.float32):
+    """A tensor whose extent the kernels assume without reading it (scales, shared weights):
+    refuse anything but exactly ``shape`` before a launch could read past it."""
+    _req(t, name, dtype)
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def _req_rows(t: torch.Tensor, name: str, rows: int):
+    if t.shape[0] < rows:
+        raise ValueError(f"{name} has {t.shape[0]} rows, max_rows={rows} needs at least that many")
+
+
 def router_topk(logits: torch.Tensor, top_k: int, renormalize: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
     """modeling_qwen3_moe.py:255-266 -> (ids int32 [T,k], weights fp32 [T,k])."""
     _req(logits, "logits", torch.float32, 2)
@@ -216,8 +229,13 @@ def gemm_gate_up_silu(a: torch.Tensor, w_gate_up: torch.Tensor, seg_offsets: tor
         raise ValueError(f"a has {a.shape[1]} columns, weights expect H={H}")
     if a_rows is not None:
         _req(a_rows, "a_rows", torch.int32)
+        _req_rows(a_rows, "a_rows", max_rows)
+    else:
+        _req_rows(a, "a", max_rows)
+    if (w_scale is not None) != (w_gate_up.dtype == torch.float8_e4m3fn):
+        raise ValueError("fp8 weights need w_scale [E, 2I]; bf16 weights take none")
     if w_scale is not None:
-        _req(w_scale, "w_scale", torch.float32)
+        _req_shape(w_scale, "w_scale", (E, I2))
     h = torch.empty(max_rows, I, dtype=torch.bfloat16, device=a.device)
     call("eimoe_gemm_gate_up_silu", a.data_ptr(), _ptr(a_rows), a.shape[0], a.stride(0), w_gate_up.data_ptr(),
          _dt(w_gate_up),
@@ -236,6 +254,11 @@ def gemm_down(h: torch.Tensor, w_down: torch.Tensor, seg_offsets: torch.Tensor, 
     E, H, I = w_down.shape
     if h.shape[1] != I:
         raise ValueError(f"h has {h.shape[1]} columns, weights expect I={I}")
+    _req_rows(h, "h", max_rows)
+    if (w_scale is not None) != (w_down.dtype == torch.float8_e4m3fn):
+        raise ValueError("fp8 weights need w_scale [E, H]; bf16 weights take none")
+    if w_scale is not None:
+        _req_shape(w_scale, "w_scale", (E, H))
     y = torch.empty(k_split, max_rows, H, dtype=out_dtype, device=h.device)
     call("eimoe_gemm_down", h.data_ptr(), I, w_down.data_ptr(), _dt(w_down), _ptr(w_scale), H,
          seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, y.data_ptr(), _dt(y), k_split, tile,
@@ -255,8 +278,15 @@ def gemm_gate_up_silu_w8a8(aq: torch.Tensor, a_scale: torch.Tensor, w_gate_up: t
     _req(seg_offsets, "seg_offsets", torch.int32, 1)
     E, I2, H = w_gate_up.shape
     I = I2 // 2
+    if aq.shape[1] != H:
+        raise ValueError(f"aq has {aq.shape[1]} columns, weights expect H={H}")
+    _req_shape(a_scale, "a_scale", (aq.shape[0],))
+    _req_shape(w_scale, "w_scale", (E, I2))
     if a_rows is not None:
         _req(a_rows, "a_rows", torch.int32)
+        _req_rows(a_rows, "a_rows", max_rows)
+    else:
+        _req_rows(aq, "aq", max_rows)
     h = torch.empty(max_rows, I, dtype=torch.bfloat16, device=aq.device)
     call("eimoe_gemm_gate_up_silu_w8a8", aq.data_ptr(), a_scale.data_ptr(), _ptr(a_rows), aq.shape[0], aq.stride(0),
          w_gate_up.data_ptr(), w_scale.data_ptr(), H, I, seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E,
@@ -274,6 +304,12 @@ def gemm_down_w8a8(hq: torch.Tensor, h_scale: torch.Tensor, w_down: torch.Tensor
     _req(w_scale, "w_scale", torch.float32)
     _req(seg_offsets, "seg_offsets", torch.int32, 1)
     E, H, I = w_down.shape
+    if hq.shape[1] != I:
+        raise ValueError(f"hq has {hq.shape[1]} columns, weights expect I={I}")
+    _req_rows(hq, "hq", max_rows)
+    if h_scale.dim() != 1 or h_scale.shape[0] < max_rows:
+        raise ValueError(f"h_scale must be 1-D with at least max_rows={max_rows} entries, got {tuple(h_scale.shape)}")
+    _req_shape(w_scale, "w_scale", (E, H))
     y = torch.empty(k_split, max_rows, H, dtype=out_dtype, device=hq.device)
     call("eimoe_gemm_down_w8a8", hq.data_ptr(), h_scale.data_ptr(), I, w_down.data_ptr(), w_scale.data_ptr(), H,
          seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, y.data_ptr(), _dt(y), k_split, tile,
@@ -289,6 +325,17 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg_offsets: torch.Tensor, ma
     _req(b, "b", (torch.bfloat16, torch.float8_e4m3fn), 3)
     _req(seg_offsets, "seg_offsets", torch.int32, 1)
     E, N, K = b.shape
+    if a.shape[1] != K:
+        raise ValueError(f"a has {a.shape[1]} columns, b expects K={K}")
+    if a_rows is not None:
+        _req(a_rows, "a_rows", torch.int32)
+        _req_rows(a_rows, "a_rows", max_rows)
+    else:
+        _req_rows(a, "a", max_rows)
+    if (b_scale is not None) != (b.dtype == torch.float8_e4m3fn):
+        raise ValueError("fp8 b needs b_scale [E, N]; bf16 b takes none")
+    if b_scale is not None:
+        _req_shape(b_scale, "b_scale", (E, N))
     c = torch.empty(max_rows, N, dtype=out_dtype, device=a.device)
     call("eimoe_grouped_gemm", a.data_ptr(), _ptr(a_rows), a.shape[0], a.stride(0), b.data_ptr(), _dt(b),
          _ptr(b_scale),
@@ -307,8 +354,12 @@ def combine(y: torch.Tensor, pos: torch.Tensor, topk_weights: torch.Tensor, shar
     _req(pos, "pos", torch.int32)
     T, k = topk_weights.shape
     n_split, rows, H = y.shape
+    if pos.numel() != T * k:
+        raise ValueError(f"pos has {pos.numel()} entries, topk_weights {T}x{k}")
     if shared_y is not None:
         _req(shared_y, "shared_y", (torch.float32, torch.bfloat16), 2)
+        if tuple(shared_y.shape) != (T, H):
+            raise ValueError(f"shared_y must be [{T}, {H}], got {tuple(shared_y.shape)}")
     out = torch.empty(T, H, dtype=out_dtype, device=y.device)
     call("eimoe_combine", y.data_ptr(), _dt(y), n_split, rows * H, pos.data_ptr(), topk_weights.data_ptr(), T, k, H,
          _ptr(shared_y), _dt(shared_y) if shared_y is not None else 0, out.data_ptr(), _dt(out), _stream(y))
@@ -340,7 +391,8 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
               w_down: torch.Tensor, *, renormalize: bool = True, shared_gate_up: Optional[torch.Tensor] = None,
               shared_down: Optional[torch.Tensor] = None, expert_range: Optional[Sequence[int]] = None,
               w_scales: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, out_dtype=None, y_fp32: bool = False,
-              w8a8: bool = False, workspace: Optional[torch.Tensor] = None, return_routing: bool = False,
+              w8a8: bool = False, h_split: bool = False, workspace: Optional[torch.Tensor] = None,
+              return_routing: bool = False,
               scoring_func: str = "softmax", n_group: int = 1, topk_group: int = 1,
               e_score_correction_bias: Optional[torch.Tensor] = None, routed_scaling_factor: float = 1.0,
               routing: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, num_experts: Optional[int] = None):
@@ -358,6 +410,9 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     the bf16 MFMA (W8A16), or with ``w8a8=True`` activations quantised per token / per row
     and both GEMMs on the fp8 MFMA (W8A8).
     fp32 hidden states are rounded to bf16 for the MFMA path.
+    ``h_split=True`` is the precise mode: h = silu(g)*u is kept as a pair of bf16 terms (hi + lo)
+    and the down projection runs once per term, so h carries ~16 significant bits instead of 8
+    (twice the down projection's time; per-assignment outputs in fp32).
     ``scoring_func="sigmoid"`` routes with the DeepSeek-V3 gate (``router_grouped_topk``:
     ``n_group``, ``topk_group``, ``e_score_correction_bias``, ``routed_scaling_factor``,
     ``renormalize`` as norm_topk_prob) instead of softmax top-k.  ``routing=(ids int32 [T,k],
@@ -392,15 +447,24 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     fp8 = w_gate_up.dtype == torch.float8_e4m3fn
     if fp8 != (w_down.dtype == torch.float8_e4m3fn) or fp8 != (w_scales is not None):
         raise ValueError("fp8 weights need both tensors in e4m3fn and w_scales=(s_gate_up, s_down)")
+    if fp8:
+        _req_shape(w_scales[0], "w_scales[0] (gate/up)", (n_local, I2))
+        _req_shape(w_scales[1], "w_scales[1] (down)", (n_local, H))
     out_dtype = out_dtype or hidden_states.dtype
     Is = 0
+    if (shared_gate_up is None) != (shared_down is None):
+        raise ValueError("shared experts need both shared_gate_up [2*Is, H] and shared_down [H, Is]")
     if shared_gate_up is not None:
-        _req(shared_gate_up, "shared_gate_up", torch.bfloat16, 2)
         _req(shared_down, "shared_down", torch.bfloat16, 2)
         Is = shared_down.shape[1]
+        _req_shape(shared_gate_up, "shared_gate_up", (2 * Is, H), torch.bfloat16)
+        _req_shape(shared_down, "shared_down", (H, Is), torch.bfloat16)
     if w8a8 and not fp8:
         raise ValueError("w8a8 needs fp8 weights and w_scales")
+    if w8a8 and h_split:
+        raise ValueError("h_split keeps h as bf16 terms; w8a8 quantises it to fp8")
     flags = (_lib.RENORMALIZE if renormalize else 0) | (_lib.Y_F32 if y_fp32 else 0) | (_lib.W8A8 if w8a8 else 0)
+    flags |= _lib.H_SPLIT if h_split else 0
     if routing is not None:
         ids_in, w_in = routing
         _req(ids_in, "routing ids", torch.int32, 2)

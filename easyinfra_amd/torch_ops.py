@@ -6,44 +6,76 @@ EasyInfra loads ``*.so`` op libraries and calls
 contiguous blocks, ``B_list`` one ``[N,K]`` nn.Linear weight per block,
 ``out[rows_i] = A[rows_i] @ B_i^T``.  Importing this module registers
 ``torch.ops.ops.hip_grouped_gemm_single`` with that schema, backed by the HIP
-grouped GEMM (the weights are stacked into ``[n_blocks, N, K]`` per call unless the
-list already consists of consecutive views of one stacked tensor).
+grouped GEMM.  The weights are read where they lie, through a device table of
+per-expert pointers: the reference's list holds its experts' Parameters repeated
+ep_size times (single_group_gemm_moe.py:73-76, 89), so only the first period goes
+into the table and the blocks index it modulo its length.  No weight is copied.
 """
 from __future__ import annotations
 
-from typing import List
+from typing import Dict, List, Tuple
 
 import torch
 
-from . import ops
+from . import _lib, ops
+from ._lib import call
 
 _LIB = torch.library.Library("ops", "FRAGMENT")
 _LIB.define("hip_grouped_gemm_single(Tensor A, Tensor[] B_list, int[] block_sizes) -> Tensor")
 
+# device pointer tables, keyed on (device index, the weights' addresses); a few bytes each
+_PTR_TABLES: Dict[Tuple[int, Tuple[int, ...]], torch.Tensor] = {}
+_MAX_TABLES = 256
 
-def _stack_weights(b_list: List[torch.Tensor]) -> torch.Tensor:
-    b0 = b_list[0]
-    N, K = b0.shape
-    base = b0.untyped_storage().data_ptr()
-    contiguous_views = all(b.is_contiguous() and b.shape == b0.shape and b.dtype == b0.dtype and
-                           b.untyped_storage().data_ptr() == base and
-                           b.data_ptr() == b0.data_ptr() + i * N * K * b0.element_size()
-                           for i, b in enumerate(b_list))
-    if contiguous_views:
-        return torch.as_strided(b0, (len(b_list), N, K), (N * K, K, 1))
-    return torch.stack([b.contiguous() for b in b_list], 0)
+
+def _period(b_list: List[torch.Tensor]) -> int:
+    """Shortest p with b_list[i] the same tensor memory as b_list[i % p] for every i."""
+    n = len(b_list)
+    ptrs = [b.data_ptr() for b in b_list]
+    for p in range(1, n + 1):
+        if n % p == 0 and all(ptrs[i] == ptrs[i % p] for i in range(n)):
+            return p
+    return n
+
+
+def _ptr_table(b_list: List[torch.Tensor], device: torch.device) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           tuple(b.data_ptr() for b in b_list))
+    t = _PTR_TABLES.get(key)
+    if t is None:
+        if len(_PTR_TABLES) >= _MAX_TABLES:
+            _PTR_TABLES.pop(next(iter(_PTR_TABLES)))
+        t = torch.tensor(key[1], dtype=torch.int64).to(device)
+        _PTR_TABLES[key] = t
+    return t
 
 
 def hip_grouped_gemm_single(A: torch.Tensor, B_list: List[torch.Tensor], block_sizes: List[int]) -> torch.Tensor:
     if len(B_list) != len(block_sizes):
         raise ValueError(f"{len(B_list)} weights for {len(block_sizes)} blocks")
+    if not B_list:
+        raise ValueError("empty B_list")
     M = int(sum(block_sizes))
     if M != A.shape[0]:
         raise ValueError(f"block sizes sum to {M}, A has {A.shape[0]} rows")
-    b = _stack_weights(B_list)
+    A = A.contiguous()
+    ops._req(A, "A", torch.bfloat16, 2)
+    N, K = B_list[0].shape
+    for i, b in enumerate(B_list):
+        ops._req(b, f"B_list[{i}]", torch.bfloat16, 2)
+        if tuple(b.shape) != (N, K) or b.device != A.device:
+            raise ValueError(f"B_list[{i}] is {tuple(b.shape)} on {b.device}, expected ({N}, {K}) on {A.device}")
+    if K != A.shape[1]:
+        raise ValueError(f"A has {A.shape[1]} columns, the weights K={K}")
+    p = _period(B_list)
+    table = _ptr_table(B_list[:p], A.device)
     off = torch.zeros(len(block_sizes) + 1, dtype=torch.int32)
     off[1:] = torch.cumsum(torch.tensor(block_sizes, dtype=torch.int64), 0).to(torch.int32)
-    return ops.grouped_gemm(A.contiguous(), b, off.to(A.device), M, out_dtype=A.dtype)
+    off = off.to(A.device)
+    c = torch.empty(M, N, dtype=A.dtype, device=A.device)
+    call("eimoe_grouped_gemm_ptrs", A.data_ptr(), None, A.shape[0], A.stride(0), table.data_ptr(), p, N, K,
+         off.data_ptr(), len(block_sizes), p, M, c.data_ptr(), _lib.BF16, 0, ops._stream(A))
+    return c
 
 
 _LIB.impl("hip_grouped_gemm_single", hip_grouped_gemm_single, "CUDA")

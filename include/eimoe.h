@@ -46,8 +46,11 @@ enum {
   EIMOE_RENORMALIZE = 1, /* renormalise the top-k weights (norm_topk_prob) */
   EIMOE_Y_F32 = 2,       /* keep the per-assignment expert outputs in fp32 (default: output dtype) */
   EIMOE_W8A8 = 4,        /* fp8 weights: also quantise activations per token and run the fp8 MFMA */
-  EIMOE_ROUTING_IN = 8   /* topk_ids / topk_w are inputs (routing done by the caller, e.g. with
+  EIMOE_ROUTING_IN = 8,  /* topk_ids / topk_w are inputs (routing done by the caller, e.g. with
                             eimoe_router_grouped_topk); logits are not read and may be NULL */
+  EIMOE_H_SPLIT = 16     /* precise mode: the SiLU*mul intermediate h is kept as two bf16 terms
+                            (h = hi + lo, ~16 significant bits instead of 8) and the down projection
+                            runs once per term (twice its time); y is kept in fp32.  Not with W8A8. */
 };
 
 /* tile selector for the GEMM entry points (0 = automatic).  EIMOE_TILE_STREAM is the
@@ -173,6 +176,15 @@ int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int ld
                        const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
                        int n_seg, int e_mod, int max_rows, void* c, int c_dtype, int tile, void* stream);
 
+/* The same grouped GEMM over separate per-expert weight tensors, read where they lie: b_ptrs is a
+ * DEVICE array of n_b pointers, b_ptrs[e] a bf16 [N, K] row-major matrix (nn.Linear layout).
+ * The reference hands the op a Python list of per-expert Parameters, repeated ep_size times
+ * (single_group_gemm_moe.py:73-76, 89); pass the n_b distinct ones with e_mod = n_b instead of
+ * stacking them (a copy of every expert's weights per call). */
+int eimoe_grouped_gemm_ptrs(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* const* b_ptrs,
+                            int n_b, int N, int K, const int32_t* seg_offsets, int n_seg, int e_mod, int max_rows,
+                            void* c, int c_dtype, int tile, void* stream);
+
 /* Weighted top-k combine: out[t,:] = sum_j w[t,j] * sum_s y[s][pos[t*k+j],:]  (+ shared_y[t,:]).
  * Replaces _all2all_chunk_output_compute (blocks/moe/moe_all2all.py:291-307) and the shared-expert
  * residual add (moe_all2all.py:535-537).  Slots with pos < 0 contribute nothing; a token with no
@@ -192,11 +204,11 @@ int eimoe_quantize_rows_fp8(const void* x, int dtype, long long rows, int cols, 
  *   residual_out = residual + hidden                        (bf16; _add_to_residual,
  *                                                            generation/utils/compute_utils.py:14)
  *   normed = norm_w * bf16(r * rsqrt(mean(r^2) + eps))       (bf16, r = residual_out in fp32;
- *                                                            _rmsnorm, modules/norms/base_rmsnorm.py:6-12)
+ *                                                            _rmsnorm, generation/modules/rmsnorm/base_rmsnorm.py:6-12)
  *   logits = normed . gate_w^T                               (fp32 accumulation; the router gate)
  * in the order of MoeAll2AllBlock.all2all_chunk_routing_compute (blocks/moe/moe_all2all.py:329-336).
  * EIMOE_LOGITS_BF16 rounds the logits to bf16 values (the Qwen3 / Mixtral gate is an F.linear
- * in bf16, modules/linears/base_linear.py:28-36); without it they stay fp32 (DeepseekV3MoEGate,
+ * in bf16, generation/modules/linear/base_linear.py:28-36); without it they stay fp32 (DeepseekV3MoEGate,
  * models/deepseek_v3/modeling_deepseek_v3.py:155-157).
  *   hidden, residual, residual_out, normed [T,H] bf16; norm_w [H] bf16; gate_w [E,H] bf16;
  *   logits [T,E] fp32.  64 <= H <= 8192, H % 64 == 0; E <= 32 with E*H*2 <= 128 KiB (one pass),

@@ -335,27 +335,33 @@ def quantize_weights_fp8(w: torch.Tensor):
     return q.view(E, N, K), s.view(E, N)
 
 
+def gate_up_fp8(xs, wq_gu, s_gu, mode: str = "w8a8") -> torch.Tensor:
+    """The fp8 gate/up projection of one expert, fp32 [rows, 2I] (before SiLU*mul).
+
+    w8a16: gu = (x @ Wq^T) * s_gu[None, :], x in bf16-exact fp32.
+    w8a8:  x quantised per token first: gu = (xq @ Wq^T) * s_x[:, None] * s_gu[None, :].
+    """
+    wgu = wq_gu.float()
+    if mode == "w8a8":
+        xq, sx = quantize_rows_fp8(xs)
+        return (xq.float() @ wgu.T) * sx[:, None] * s_gu[None, :]
+    return (xs.float() @ wgu.T) * s_gu[None, :]
+
+
 def expert_mlp_fp8(xs, wq_gu, s_gu, wq_d, s_d, mode: str = "w8a8") -> torch.Tensor:
     """One expert with fp8 weights.
 
-    w8a16: y = ((x @ Wq_gu^T) * s_gu -> silu*mul) @ Wq_d^T * s_d, activations in
-           bf16-exact fp32.
-    w8a8:  activations dynamically quantised per token before each GEMM:
-           gu = (xq @ Wq^T) * s_x[:,None] * s_gu[None,:]; h likewise with its row scale.
+    w8a16: y = (silu(g)*u rounded to bf16) @ Wq_d^T * s_d, gate/up as in ``gate_up_fp8``.
+    w8a8:  h = silu(g)*u is stored in bf16 (the expert path's intermediate precision) and
+           quantised per row from that copy: y = (hq @ Wq_d^T) * s_h[:, None] * s_d[None, :].
     """
     I = wq_d.shape[1]
-    wgu = wq_gu.float()
     wd = wq_d.float()
-    if mode == "w8a8":
-        xq, sx = quantize_rows_fp8(xs)
-        gu = (xq.float() @ wgu.T) * sx[:, None] * s_gu[None, :]
-    else:
-        gu = (xs.float() @ wgu.T) * s_gu[None, :]
-    h = silu(gu[:, :I]) * gu[:, I:]
+    gu = gate_up_fp8(xs, wq_gu, s_gu, mode)
+    h = _round_bf16(silu(gu[:, :I]) * gu[:, I:])
     if mode == "w8a8":
         hq, sh = quantize_rows_fp8(h)
         return (hq.float() @ wd.T) * sh[:, None] * s_d[None, :]
-    h = _round_bf16(h)
     return (h @ wd.T) * s_d[None, :]
 
 

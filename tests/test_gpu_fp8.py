@@ -1,11 +1,13 @@
 """fp8 paths on the GPU.
 
 W8A8 (fp8 activations and weights on the fp8 MFMA): each GEMM is compared with the
-oracle on the same quantised operands (tight: only fp32 accumulation order and
-bf16 storage of h differ), and the layer with the oracle's W8A8 forward.  Against
-the bf16 fp32 reference the W8A8 layer carries e4m3 rounding of both operands of
-both GEMMs (~6.5% rel-L2 on N(0,0.02) weights), which is reported, not asserted
-at 5e-2; the W8A16 layer meets 5e-2.
+oracle on the same quantised operands (tight: only fp32 accumulation order differs),
+and the layer with the oracle's W8A8 forward (1e-2).  Against the bf16 fp32
+reference the W8A8 layer carries e4m3 rounding of both operands of both GEMMs:
+6.5 % rel-L2 at the Mixtral shape, which the stated 5e-2 cannot hold (rounding x
+and W_gate_up alone exceeds it, tests/test_oracle.py pins that on the CPU), so the
+W8A8 layer is held to the measured e4m3 floor with margin (7.5e-2).  The W8A16 layer
+(fp8 weights, bf16 activations) meets 5e-2.
 """
 import numpy as np
 import pytest
@@ -90,11 +92,11 @@ def test_w8a8_layer(dev, name, T):
                                   expert_range=inp.expert_range)
     ref = oracle.moe_forward(inp.x, inp.logits, s.top_k, inp.w_gate_up, inp.w_down, s.renormalize,
                              expert_range=inp.expert_range)
-    # h is quantised from its bf16 copy on the GPU and from fp32 in the oracle: a few e4m3
-    # values round differently, hence a looser bound than the GEMM checks above.
-    assert oracle.rel_l2(got, ref8) <= 3e-2
+    # h is quantised from its bf16 copy on both sides; fp32 accumulation order can still flip a
+    # rare bf16 / e4m3 rounding, hence a looser bound than the GEMM checks above.
+    assert oracle.rel_l2(got, ref8) <= 1e-2
     print(f"{name} T={T}: W8A8 vs W8A8-oracle {oracle.rel_l2(got, ref8):.3e}, vs bf16-ref {oracle.rel_l2(got, ref):.3e}")
-    assert oracle.rel_l2(got, ref) <= 1e-1
+    assert oracle.rel_l2(got, ref) <= 7.5e-2
 
 
 def test_w8a16_layer_meets_fp8_tolerance(dev):
@@ -112,19 +114,23 @@ def test_w8a16_layer_meets_fp8_tolerance(dev):
 @pytest.mark.slow
 @pytest.mark.parametrize("T", [64, 8192])
 def test_fp8_mixtral_real_shape(dev, T):
-    """Mixtral-8x7B with fp8-e4m3 weights (per-channel absmax/448) against the bf16 fp32 reference."""
+    """Mixtral-8x7B with fp8-e4m3 weights (per-channel absmax/448), every row, against the bf16
+    fp32 reference and against the oracle's own fp8 forward of the same mode."""
+    import json
     inp = make_inputs(SHAPES["mixtral-8x7b-fp8"], T, device=dev)
-    s = inp.shape
     qgu, sgu = ops.quantize_weights_fp8(inp.w_gate_up)
     qd, sd = ops.quantize_weights_fp8(inp.w_down)
-    sub = torch.randperm(T, generator=torch.Generator().manual_seed(T))[:16]
-    ref = oracle.moe_forward(cpu(inp.x), cpu(inp.logits), 2, cpu(inp.w_gate_up), cpu(inp.w_down), True,
-                             token_subset=sub)
+    x, lg = cpu(inp.x), cpu(inp.logits)
+    ref = oracle.moe_forward(x, lg, 2, cpu(inp.w_gate_up), cpu(inp.w_down), True)
     res = {}
     for mode in ("w8a16", "w8a8"):
-        out = ops.fused_moe(inp.x, inp.logits, 2, qgu, qd, w_scales=(sgu, sd), out_dtype=torch.float32,
-                            w8a8=(mode == "w8a8"))
-        res[mode] = oracle.rel_l2(cpu(out)[sub], ref)
-    print(f"fp8 mixtral T={T}: rel-L2 vs bf16 reference {res}")
-    assert res["w8a16"] <= 5e-2
-    assert res["w8a8"] <= 1e-1
+        out = cpu(ops.fused_moe(inp.x, inp.logits, 2, qgu, qd, w_scales=(sgu, sd), out_dtype=torch.float32,
+                                w8a8=(mode == "w8a8")))
+        own = oracle.moe_forward_fp8(x, lg, 2, cpu(qgu), cpu(sgu), cpu(qd), cpu(sd), True, mode=mode)
+        res[mode] = (oracle.rel_l2(out, ref), oracle.rel_l2(out, own))
+        print("PARITY " + json.dumps({"case": f"mixtral-8x7b-fp8 {mode} T={T}", "rows": T,
+                                      "rel_l2_vs_bf16_ref": res[mode][0], "rel_l2_vs_fp8_oracle": res[mode][1]},
+                                     sort_keys=True), flush=True)
+    assert res["w8a16"][1] <= 1e-2 and res["w8a8"][1] <= 1e-2
+    assert res["w8a16"][0] <= 5e-2
+    assert res["w8a8"][0] <= 7.5e-2

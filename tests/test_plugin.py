@@ -145,3 +145,32 @@ def test_torch_op_matches_reference_contract(dev):
     ref = oracle.grouped_gemm(a, bl, blocks)
     assert out.dtype == torch.bfloat16
     torch.testing.assert_close(out.cpu().float(), ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.gpu
+def test_torch_op_repeated_expert_list_reads_weights_in_place(dev):
+    """The reference passes its experts' weights repeated ep_size times (single_group_gemm_moe.py:73-76):
+    block i uses B_list[i]; the op must read the separate tensors where they lie (no stacked copy)."""
+    import easyinfra_amd.torch_ops as tops
+    g = torch.Generator().manual_seed(9)
+    K, N, E, ep = 256, 128, 3, 2
+    experts = [(torch.randn(N, K, generator=g) * 0.1).to(torch.bfloat16).to(dev) for _ in range(E)]
+    bl = experts * ep
+    blocks = [17, 0, 40, 3, 64, 9]
+    a = torch.randn(sum(blocks), K, generator=g).to(torch.bfloat16)
+    assert tops._period(bl) == E
+    before = torch.cuda.memory_allocated(dev)
+    out = torch.ops.ops.hip_grouped_gemm_single(a.to(dev), bl, blocks)
+    grown = torch.cuda.memory_allocated(dev) - before
+    assert grown < N * K * 2, f"op allocated {grown} bytes: looks like a weight copy"
+    ref = oracle.grouped_gemm(a, [b.cpu() for b in bl], blocks)
+    torch.testing.assert_close(out.cpu().float(), ref, rtol=1e-2, atol=1e-2)
+
+
+def test_torch_op_period_detection():
+    import easyinfra_amd.torch_ops as tops
+    a, b, c = torch.zeros(2), torch.zeros(2), torch.zeros(2)
+    assert tops._period([a, b, a, b]) == 2
+    assert tops._period([a, b, c]) == 3
+    assert tops._period([a, a, a]) == 1
+    assert tops._period([a, b, a]) == 3
