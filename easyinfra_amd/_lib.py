@@ -60,6 +60,10 @@ SIGNATURES = {
     "eimoe_fused_moe": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int,
                                 c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int,
                                 c_void_p, c_size_t, c_void_p, c_void_p, c_void_p]),
+    "eimoe_fused_moe_static_bytes": (c_size_t, []),
+    "eimoe_fused_moe_static": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                       c_int, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int,
+                                       c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
 }
 
 _lib = None

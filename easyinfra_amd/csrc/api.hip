@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "../../include/eimoe.h"
 #include "common.h"
@@ -667,11 +668,18 @@ size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_
   return fused_layout(T, H, I, E, k, n_local, shared_inter, out_dtype, flags).total;
 }
 
-int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int E, int k, const void* w_gate_up,
-                    const void* w_down, int w_dtype, const float* w_gate_up_scale, const float* w_down_scale, int e_lo,
-                    int n_local, const void* shared_gate_up, const void* shared_down, int shared_inter, int flags,
-                    void* out, int out_dtype, void* workspace, size_t workspace_bytes, int32_t* topk_ids_out,
-                    float* topk_w_out, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The fused layer over a workspace.  no_alloc: the workspace is the library's static scratch, so
+// nothing may be created here (the shared experts then run on the caller's stream rather than on
+// the second stream, which would be created on first use).
+int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int E, int k, const void* w_gate_up,
+                   const void* w_down, int w_dtype, const float* w_gate_up_scale, const float* w_down_scale, int e_lo,
+                   int n_local, const void* shared_gate_up, const void* shared_down, int shared_inter, int flags,
+                   void* out, int out_dtype, void* workspace, size_t workspace_bytes, int32_t* topk_ids_out,
+                   float* topk_w_out, void* stream, bool no_alloc) {
   if (T < 0) return fail(EIMOE_ERR_SHAPE, "T=%d < 0", T);
   if (E < 1 || E > EIMOE_MAX_EXPERTS) return fail(EIMOE_ERR_SHAPE, "E=%d outside [1,%d]", E, EIMOE_MAX_EXPERTS);
   if (k < 1 || k > E || k > EIMOE_MAX_TOPK)
@@ -723,8 +731,12 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
     REQUIRE_PTR(shared_down);
   }
   const FusedLayout L = fused_layout(T, H, I, E, k, n_local, shared_inter, out_dtype, flags);
-  if (workspace_bytes < L.total)
+  if (workspace_bytes < L.total) {
+    if (no_alloc)
+      return fail(EIMOE_ERR_WORKSPACE, "this layer needs %zu bytes of scratch; eimoe_fused_moe_static holds %zu",
+                  L.total, workspace_bytes);
     return fail(EIMOE_ERR_WORKSPACE, "workspace %zu bytes < required %zu", workspace_bytes, L.total);
+  }
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   auto at = [&](size_t off) { return static_cast<void*>(ws + off); };
   int32_t* ids = topk_ids_out ? topk_ids_out : static_cast<int32_t*>(at(L.ids));
@@ -744,9 +756,11 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   const void* sh_y = nullptr;
   AuxStream* aux = nullptr;
   if (shared_inter > 0) {
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if ((rc = hip_check(hipStreamIsCapturing(s, &cap), "capture status"))) return rc;
-    if ((rc = hip_check(aux_stream(&aux, cap == hipStreamCaptureStatusNone), "aux stream"))) return rc;
+    if (!no_alloc) {
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if ((rc = hip_check(hipStreamIsCapturing(s, &cap), "capture status"))) return rc;
+      if ((rc = hip_check(aux_stream(&aux, cap == hipStreamCaptureStatusNone), "aux stream"))) return rc;
+    }
     const hipStream_t s2 = aux ? aux->stream : s;   // no second stream yet under capture: serial
     if (aux) {
       if ((rc = hip_check(hipEventRecord(aux->fork, s), "fork"))) return rc;
@@ -834,6 +848,61 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
   return hip_check(launch_combine(at(L.y), L.y_dtype, L.h_terms * L.k_split, static_cast<long long>(A) * H, pos, w, T,
                                   k, H, sh_y, L.y_dtype, L.h_terms, out, out_dtype, s),
                    "combine");
+}
+
+// Static scratch of eimoe_fused_moe_static: every GPU the library runs on holds one copy for the
+// life of the process.  Host code never uses the array's name as an address (on the host it is a
+// stand-in, not device memory); it uses the per-device address from hipGetSymbolAddress.
+constexpr size_t kStaticScratchBytes = 64ull << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Looked up once per device, on the entry point's first call with that device current.
+int static_scratch(void** out) {
+  int dev = 0;
+  int rc = hip_check(hipGetDevice(&dev), "current device");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(EIMOE_ERR_HIP, "device %d outside [0,%d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if ((rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "static scratch address"))) return rc;
+    if (!p) return fail(EIMOE_ERR_HIP, "static scratch address is NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return EIMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int E, int k, const void* w_gate_up,
+                    const void* w_down, int w_dtype, const float* w_gate_up_scale, const float* w_down_scale, int e_lo,
+                    int n_local, const void* shared_gate_up, const void* shared_down, int shared_inter, int flags,
+                    void* out, int out_dtype, void* workspace, size_t workspace_bytes, int32_t* topk_ids_out,
+                    float* topk_w_out, void* stream) {
+  return fused_moe_impl(x, logits, T, H, I, E, k, w_gate_up, w_down, w_dtype, w_gate_up_scale, w_down_scale, e_lo,
+                        n_local, shared_gate_up, shared_down, shared_inter, flags, out, out_dtype, workspace,
+                        workspace_bytes, topk_ids_out, topk_w_out, stream, false);
+}
+
+size_t eimoe_fused_moe_static_bytes(void) { return kStaticScratchBytes; }
+
+int eimoe_fused_moe_static(const void* x, const float* logits, int T, int H, int I, int E, int k,
+                           const void* w_gate_up, const void* w_down, int w_dtype, const float* w_gate_up_scale,
+                           const float* w_down_scale, int e_lo, int n_local, const void* shared_gate_up,
+                           const void* shared_down, int shared_inter, int flags, void* out, int out_dtype,
+                           int32_t* topk_ids_out, float* topk_w_out, void* stream) {
+  void* ws = nullptr;
+  const int rc = static_scratch(&ws);
+  if (rc) return rc;
+  return fused_moe_impl(x, logits, T, H, I, E, k, w_gate_up, w_down, w_dtype, w_gate_up_scale, w_down_scale, e_lo,
+                        n_local, shared_gate_up, shared_down, shared_inter, flags, out, out_dtype, ws,
+                        kStaticScratchBytes, topk_ids_out, topk_w_out, stream, true);
 }
 
 }  // extern "C"

@@ -241,6 +241,23 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
                     void* out, int out_dtype, void* workspace, size_t workspace_bytes, int32_t* topk_ids_out,
                     float* topk_w_out, void* stream);
 
+/* eimoe_fused_moe without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments and results as eimoe_fused_moe; its scratch is a
+ * static device array of eimoe_fused_moe_static_bytes() (64 MiB) that each GPU holds from the
+ * first call until the process ends, so it fits decode-sized layers (a Mixtral-8x7B layer up to
+ * ~1k tokens; eimoe_fused_moe_workspace_bytes gives the need) and returns EIMOE_ERR_WORKSPACE,
+ * launching nothing, when a layer needs more.  It calls no hipMalloc/hipFree and creates no
+ * stream or event (shared experts run on `stream` after the routed ones).  Every call on a GPU
+ * uses that GPU's one scratch array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller. */
+size_t eimoe_fused_moe_static_bytes(void);
+int eimoe_fused_moe_static(const void* x, const float* logits, int T, int H, int I, int E, int k,
+                           const void* w_gate_up, const void* w_down, int w_dtype, const float* w_gate_up_scale,
+                           const float* w_down_scale, int e_lo, int n_local, const void* shared_gate_up,
+                           const void* shared_down, int shared_inter, int flags, void* out, int out_dtype,
+                           int32_t* topk_ids_out, float* topk_w_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
