@@ -20,7 +20,7 @@ ARCH = "gfx950"
 
 # -packed-fp32-ops off: hipcc would otherwise emit v_pk_{add,mul,fma}_f32 from plain
 # float code.  The host pass warns that it does not know the feature; harmless.
-HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+HIP_FLAGS = ["-O3", "-std=c++20", "-fPIC", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-result"]
 

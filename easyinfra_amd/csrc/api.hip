@@ -750,9 +750,21 @@ int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int 
   const hipStream_t s = S(stream);
   const int A = T * k;
   int rc;
+  // Routing first: the shared experts forked below would otherwise fill the GPU ahead of the small
+  // routing kernels on the critical path.
+  if (routing_in) {
+    if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos, hist,
+                                     s),
+                        "align")))
+      return rc;
+  } else if ((rc = hip_check(launch_route_align(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, e_lo, n_local,
+                                                ids, w, counts, offsets, sorted_flat, sorted_tok, pos, hist, s),
+                             "route_align"))) {
+    return rc;
+  }
   // Shared experts (every token, weight 1) depend only on x: fork them onto the second
-  // stream first, so they run beside the routing and the routed GEMMs; joined before the
-  // combine.
+  // stream once the routing is enqueued, so they run beside the routed GEMMs; joined before
+  // the combine.
   const void* sh_y = nullptr;
   AuxStream* aux = nullptr;
   if (shared_inter > 0) {
@@ -798,17 +810,6 @@ int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int 
   // (an early error return must not leave the second stream using the workspace unjoined).
   auto routed = [&]() -> int {
     int rc;
-    if (routing_in) {
-      if ((rc = hip_check(launch_align(ids, T, k, e_lo, n_local, counts, offsets, sorted_flat, sorted_tok, pos,
-                                       hist, s),
-                          "align")))
-        return rc;
-    } else if ((rc = hip_check(launch_route_align(logits, T, E, k, (flags & EIMOE_RENORMALIZE) ? 1 : 0, e_lo,
-                                                  n_local, ids, w, counts, offsets, sorted_flat, sorted_tok, pos, hist,
-                                                  s),
-                               "route_align"))) {
-      return rc;
-    }
     if (flags & EIMOE_W8A8) {
       // activations quantised per token (x) and per row (h); both GEMMs on the fp8 MFMA
       uint8_t* xq = static_cast<uint8_t*>(at(L.xq));

@@ -427,3 +427,75 @@ def test_fp8_weight_gemms(dev, tile):
         torch.testing.assert_close(h[a:b], href, rtol=1e-2, atol=1e-2)
         yref = (h[a:b] @ qd[e].float().T) * sd[e]
         torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
+
+
+# Segment remainders of every height class: a segment's last tile is a quarter, half or full
+# tile (256x256: 64 / 128 / 256 rows; 128x128: 32 / 64 / 128), and the last m-tile group of a
+# long segment takes the leftover tiles (10 m-tiles of 256 rows: groups of 4 and 6).
+REMAINDER_COUNTS = {1: [257, 320, 321, 128, 129, 712, 63, 9 * 256 + 2, 0],
+                    2: [33, 32, 64, 65, 129, 127, 11 * 128 + 7, 0, 1]}
+
+
+@pytest.mark.parametrize("tile", [1, 2])
+@pytest.mark.parametrize("k_split", [1, 2])
+def test_gemms_remainder_tile_heights(dev, tile, k_split):
+    counts = REMAINDER_COUNTS[tile]
+    g = torch.Generator().manual_seed(77 + tile + k_split)
+    H, I = 256, 256
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 300
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16)
+    wd = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16)
+    h = ops.gemm_gate_up_silu(x.to(dev), wgu.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev), tile=tile)
+    y = cpu(ops.gemm_down(h, wd.to(dev), off_t.to(dev), rows, out_dtype=torch.float32, k_split=k_split,
+                          tile=tile)).sum(0)
+    h = cpu(h).float()
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        gu = x[a_rows[a:b].long()].float() @ wgu[e].float().T
+        torch.testing.assert_close(h[a:b], oracle.silu(gu[:, :I]) * gu[:, I:], rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(y[a:b], h[a:b] @ wd[e].float().T, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("tile", [1, 2])
+def test_fp8_gemms_remainder_tile_heights(dev, tile):
+    """The same segment layouts on the W8A8 (fp8 x fp8) and W8A16 (fp8 weights) kernels."""
+    counts = REMAINDER_COUNTS[tile]
+    g = torch.Generator().manual_seed(91 + tile)
+    H, I = 256, 256
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 300
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
+    qgu, sgu = oracle.quantize_weights_fp8(torch.randn(E, 2 * I, H, generator=g) * 0.02)
+    qd, sd = oracle.quantize_weights_fp8(torch.randn(E, H, I, generator=g) * 0.02)
+    xq, sx = oracle.quantize_rows_fp8(x)
+    h8 = cpu(ops.gemm_gate_up_silu_w8a8(xq.to(dev), sx.to(dev), qgu.to(dev), sgu.to(dev), off_t.to(dev), rows,
+                                        a_rows=a_rows.to(dev), tile=tile)).float()
+    h16 = ops.gemm_gate_up_silu(x.to(dev), qgu.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev),
+                                w_scale=sgu.to(dev), tile=tile)
+    hq, sh = oracle.quantize_rows_fp8(h8)
+    y8 = cpu(ops.gemm_down_w8a8(hq.to(dev), sh.to(dev), qd.to(dev), sd.to(dev), off_t.to(dev), rows,
+                                tile=tile)).sum(0)
+    y16 = cpu(ops.gemm_down(h16, qd.to(dev), off_t.to(dev), rows, w_scale=sd.to(dev), tile=tile)).sum(0)
+    h16 = cpu(h16).float()
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        tok = a_rows[a:b].long()
+        gu8 = (xq[tok].float() @ qgu[e].float().T) * sx[tok][:, None] * sgu[e][None, :]
+        torch.testing.assert_close(h8[a:b], oracle.silu(gu8[:, :I]) * gu8[:, I:], rtol=1e-2, atol=1e-2)
+        gu16 = (x[tok].float() @ qgu[e].float().T) * sgu[e][None, :]
+        torch.testing.assert_close(h16[a:b], oracle.silu(gu16[:, :I]) * gu16[:, I:], rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(y8[a:b], (hq[a:b].float() @ qd[e].float().T) * sh[a:b][:, None] * sd[e][None, :],
+                                   rtol=1e-4, atol=1e-4)
+        torch.testing.assert_close(y16[a:b], (h16[a:b] @ qd[e].float().T) * sd[e][None, :], rtol=1e-3, atol=1e-3)
