@@ -34,6 +34,7 @@ sys.path.insert(0, str(ROOT))
 
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 FP8_PEAK_TFLOPS = 5000.0
+FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 METRIC = "MoE-layer tokens/s + TFLOP/s (% MFMA peak) on 1 MI355X; vs host-CPU ref"
 
@@ -216,8 +217,10 @@ def layer_case(name, inp, torch, ops, steps, warmup, flush, *, w8a8=False, fp8w=
     Is = inp.shared_down.shape[1] if inp.shared_down is not None else 0
     kw = dict(renormalize=s.renormalize, shared_gate_up=inp.shared_gate_up, shared_down=inp.shared_down,
               expert_range=inp.expert_range, w_scales=scales, w8a8=w8a8, **(router_kw or {}))
-    ws = torch.empty(ops.fused_moe_workspace_bytes(T, H, I, s.n_experts, s.top_k, n_local, Is,
-                                                   flags=4 if w8a8 else 0), dtype=torch.uint8, device=inp.x.device)
+    f32 = wgu.dtype == torch.float32
+    flags = 4 if w8a8 else 32 if f32 else 0
+    ws = torch.empty(ops.fused_moe_workspace_bytes(T, H, I, s.n_experts, s.top_k, n_local, Is, out_dtype=inp.x.dtype,
+                                                   flags=flags), dtype=torch.uint8, device=inp.x.device)
     fn = lambda: ops.fused_moe(inp.x, inp.logits, s.top_k, wgu, wd, workspace=ws, **kw)
     _, ids, _ = ops.fused_moe(inp.x, inp.logits, s.top_k, wgu, wd, return_routing=True, **kw)
     lo, hi = inp.expert_range or (0, s.n_experts)
@@ -228,9 +231,10 @@ def layer_case(name, inp, torch, ops, steps, warmup, flush, *, w8a8=False, fp8w=
     ms = timed(fn, steps, warmup, torch)
     ms_cold = timed_cold(fn, steps, 1, torch, flush)
     flops = layer_flops(A, T, H, I, Is)
-    b_w = 1 if fp8w is not None else 2
-    nbytes = layer_bytes(touched, T, s.n_experts, H, I, b_w, 2, 2, Is, fp8_scales=fp8w is not None)
-    peak = FP8_PEAK_TFLOPS if w8a8 else BF16_PEAK_TFLOPS
+    b_w = 1 if fp8w is not None else 4 if f32 else 2
+    b_x = 4 if f32 else 2
+    nbytes = layer_bytes(touched, T, s.n_experts, H, I, b_w, b_x, b_x, Is, fp8_scales=fp8w is not None)
+    peak = FP8_PEAK_TFLOPS if w8a8 else FP32_PEAK_TFLOPS if f32 else BF16_PEAK_TFLOPS
     return {"case": name, "tokens": T, "assignments": A, "touched_experts": touched, "ms": round(ms, 4),
             "ms_cold": round(ms_cold, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
             "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / peak, 4),
@@ -282,8 +286,7 @@ def suite(torch, ops, mix_inp, steps, warmup):
     flush = torch.ones(128 << 20, dtype=torch.float32, device=dev)   # 512 MB > the 256 MB last-level cache
     out = []
     inp = make_inputs(SHAPES["tiny-mixtral-fp32"], 512, device=dev)
-    inp.w_gate_up, inp.w_down = inp.w_gate_up.to(torch.bfloat16), inp.w_down.to(torch.bfloat16)
-    out.append(layer_case("tiny-mixtral-fp32 T=512 (bf16 MFMA)", inp, torch, ops, steps, warmup, flush))
+    out.append(layer_case("tiny-mixtral-fp32 T=512 (fp32 layer, fp32 MFMA)", inp, torch, ops, steps, warmup, flush))
     del inp
     ds = SHAPES["deepseek-v2-lite"]
     skew = layer_case("deepseek-v2-lite T=4096 zipf(1.2) + 2 shared", make_inputs(ds, 4096, device=dev), torch, ops,

@@ -14,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libeimoe.so")
 EIMOE_OK = 0
 ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_WORKSPACE, ERR_HIP = -1, -2, -3, -4, -5, -6
 F32, BF16, FP8 = 0, 1, 2
-RENORMALIZE, Y_F32, W8A8, ROUTING_IN, H_SPLIT = 1, 2, 4, 8, 16
+RENORMALIZE, Y_F32, W8A8, ROUTING_IN, H_SPLIT, FP32 = 1, 2, 4, 8, 16, 32
 LOGITS_BF16 = 1   # eimoe_moe_prologue flag
 TILE_AUTO, TILE_256x256, TILE_128x128, TILE_32x128, TILE_16x64, TILE_STREAM = 0, 1, 2, 3, 4, 5
 MAX_TOPK, MAX_EXPERTS, MAX_SEGMENTS = 32, 512, 1024

@@ -173,7 +173,9 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   const size_t A = static_cast<size_t>(T) * k;
   L.rows_hint = local_rows_hint(T, k, E, n_local);
   L.h_terms = (flags & EIMOE_H_SPLIT) ? 2 : 1;
-  L.y_dtype = ((flags & (EIMOE_Y_F32 | EIMOE_H_SPLIT)) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
+  L.y_dtype =
+      ((flags & (EIMOE_Y_F32 | EIMOE_H_SPLIT | EIMOE_FP32)) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
+  const size_t hb = (flags & EIMOE_FP32) ? 4 : 2;   // bytes per h element
   L.k_split = pick_down_split(static_cast<int>(A), L.rows_hint, n_local, H, I,
                               static_cast<int>(elem_size(L.y_dtype)), (flags & EIMOE_W8A8) != 0);
   size_t o = 0;
@@ -190,7 +192,7 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   L.sorted_tok = take(A * 4);
   L.pos = take(A * 4);
   L.hist = take(align_plan(static_cast<int>(A), n_local).hist_ints * 4);
-  L.h = take(A * I * 2);
+  L.h = take(A * I * hb);
   if (L.h_terms == 2) L.h_lo = take(A * I * 2);
   L.y = take(static_cast<size_t>(L.h_terms) * L.k_split * A * H * elem_size(L.y_dtype));
   if (flags & EIMOE_W8A8) {
@@ -201,7 +203,7 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   }
   if (Is > 0) {
     L.sh_off = take(2 * 4);
-    L.sh_h = take(static_cast<size_t>(T) * Is * 2);
+    L.sh_h = take(static_cast<size_t>(T) * Is * hb);
     if (L.h_terms == 2) L.sh_h_lo = take(static_cast<size_t>(T) * Is * 2);
     L.sh_y = take(static_cast<size_t>(L.h_terms) * T * H * elem_size(L.y_dtype));
   }
@@ -243,6 +245,7 @@ int run_gate_up(const void* a, const int32_t* a_rows, long long a_nrows, int lda
   p.max_rows = max_rows;
   p.a_rows_cap = a_rows ? a_nrows : max_rows;
   p.a_scale = a_scale;
+  if (w_dtype == EIMOE_F32) return hip_check(launch_grouped_gemm_f32(p, kEpiSiluF32, max_rows, tile, s), "gate_up gemm");
   return hip_check(launch_grouped_gemm(p, kEpiSiluBF16, w_dtype == EIMOE_FP8, a_scale != nullptr, max_rows, tile, s),
                    "gate_up gemm");
 }
@@ -274,6 +277,7 @@ int run_down(const void* h, int I, const void* w, int w_dtype, const float* w_sc
   p.a_rows_cap = max_rows;
   p.a_scale = h_scale;
   const int epi = y_dtype == EIMOE_F32 ? kEpiStoreF32 : kEpiStoreBF16;
+  if (w_dtype == EIMOE_F32) return hip_check(launch_grouped_gemm_f32(p, epi, max_rows, tile, s), "down gemm");
   return hip_check(launch_grouped_gemm(p, epi, w_dtype == EIMOE_FP8, h_scale != nullptr, max_rows, tile, s),
                    "down gemm");
 }
@@ -421,18 +425,20 @@ int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int a_nrows, i
                             int max_rows, void* h, int tile, void* stream) {
   int rc = check_gemm_common(max_rows, n_seg, e_mod);
   if (rc) return rc;
-  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
+  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8 && w_dtype != EIMOE_F32)
+    return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
   if (H < 64 || H % 64) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 64", H);
   if (I < 32 || I % 32) return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 32", I);
   if (lda < H) return fail(EIMOE_ERR_SHAPE, "lda=%d < H=%d", lda, H);
   if (a_rows && a_nrows < 1) return fail(EIMOE_ERR_SHAPE, "a_nrows=%d < 1 with a row map", a_nrows);
   if (!a_rows) a_nrows = max_rows;
-  if (static_cast<long long>(a_nrows) * lda * 2 > 0x7fffffffll)
+  const long long ab = w_dtype == EIMOE_F32 ? 4 : 2;   // fp32 weights take fp32 activations
+  if (static_cast<long long>(a_nrows) * lda * ab > 0x7fffffffll)
     return fail(EIMOE_ERR_SHAPE, "A buffer (%d rows x %d) exceeds 2 GiB", a_nrows, lda);
-  if (static_cast<long long>(e_mod) * 2 * I * H * (w_dtype == EIMOE_FP8 ? 1 : 2) < 0)
-    return fail(EIMOE_ERR_SHAPE, "weight size overflows");
-  if (2ll * I * H * (w_dtype == EIMOE_FP8 ? 1 : 2) > 0x7fffffffll)
+  if (2ll * I * H * elem_size(w_dtype) > 0x7fffffffll)
     return fail(EIMOE_ERR_SHAPE, "one expert's gate/up weights exceed 2 GiB");
+  if (w_dtype == EIMOE_F32 && static_cast<long long>(max_rows) * I * 4 > 0x7fffffffll)
+    return fail(EIMOE_ERR_SHAPE, "h (%d rows x %d, fp32) exceeds 2 GiB", max_rows, I);
   if (lda % 8) return fail(EIMOE_ERR_ALIGN, "lda=%d must be a multiple of 8", lda);
   if ((rc = check_tile(tile, kEpiSiluBF16, I))) return rc;
   if (max_rows == 0) return EIMOE_OK;
@@ -450,16 +456,18 @@ int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const
                     int k_split, int tile, void* stream) {
   int rc = check_gemm_common(max_rows, n_seg, e_mod);
   if (rc) return rc;
-  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
+  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8 && w_dtype != EIMOE_F32)
+    return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
   if (y_dtype != EIMOE_BF16 && y_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "y_dtype=%d", y_dtype);
+  if (w_dtype == EIMOE_F32 && y_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "fp32 weights write fp32 y");
   if (H < 64 || H % 64) return fail(EIMOE_ERR_ALIGN, "H=%d must be a positive multiple of 64", H);
   if (k_split < 1 || k_split > 64) return fail(EIMOE_ERR_SHAPE, "k_split=%d outside [1,64]", k_split);
   if (I < 64 || I % (64 * k_split))
     return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 64*k_split=%d", I, 64 * k_split);
   if ((rc = check_tile(tile, kEpiStoreF32, H))) return rc;
-  if (static_cast<long long>(max_rows) * I * 2 > 0x7fffffffll)
+  if (static_cast<long long>(max_rows) * I * (w_dtype == EIMOE_F32 ? 4 : 2) > 0x7fffffffll)
     return fail(EIMOE_ERR_SHAPE, "h (%d rows x %d) exceeds 2 GiB", max_rows, I);
-  if (static_cast<long long>(H) * I * (w_dtype == EIMOE_FP8 ? 1 : 2) > 0x7fffffffll)
+  if (static_cast<long long>(H) * I * elem_size(w_dtype) > 0x7fffffffll)
     return fail(EIMOE_ERR_SHAPE, "one expert's down weights exceed 2 GiB");
   if (max_rows == 0) return EIMOE_OK;
   REQUIRE_PTR(h);
@@ -529,18 +537,20 @@ int grouped_gemm_impl(const void* a, const int32_t* a_rows, int a_nrows, int lda
                       int tile, void* stream) {
   int rc = check_gemm_common(max_rows, n_seg, e_mod);
   if (rc) return rc;
-  if (b_dtype != EIMOE_BF16 && b_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "b_dtype=%d", b_dtype);
+  if (b_dtype != EIMOE_BF16 && b_dtype != EIMOE_FP8 && b_dtype != EIMOE_F32)
+    return fail(EIMOE_ERR_DTYPE, "b_dtype=%d", b_dtype);
   if (c_dtype != EIMOE_BF16 && c_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "c_dtype=%d", c_dtype);
+  if (b_dtype == EIMOE_F32 && c_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "fp32 b writes fp32 c");
   if (K < 64 || K % 64) return fail(EIMOE_ERR_ALIGN, "K=%d must be a positive multiple of 64", K);
   if (N < 64 || N % 64) return fail(EIMOE_ERR_ALIGN, "N=%d must be a positive multiple of 64", N);
   if (lda < K || lda % 8) return fail(EIMOE_ERR_SHAPE, "lda=%d must be >= K=%d and a multiple of 8", lda, K);
   if (b_expert_stride < static_cast<long long>(N) * K)
     return fail(EIMOE_ERR_SHAPE, "b_expert_stride=%lld < N*K", b_expert_stride);
-  if (b_expert_stride * (b_dtype == EIMOE_FP8 ? 1 : 2) > 0x7fffffffll)
+  if (b_expert_stride * elem_size(b_dtype) > 0x7fffffffll)
     return fail(EIMOE_ERR_SHAPE, "one expert's weights exceed 2 GiB");
   if (a_rows && a_nrows < 1) return fail(EIMOE_ERR_SHAPE, "a_nrows=%d < 1 with a row map", a_nrows);
   if (!a_rows) a_nrows = max_rows;
-  if (static_cast<long long>(a_nrows) * lda * 2 > 0x7fffffffll)
+  if (static_cast<long long>(a_nrows) * lda * (b_dtype == EIMOE_F32 ? 4 : 2) > 0x7fffffffll)
     return fail(EIMOE_ERR_SHAPE, "A buffer (%d rows x %d) exceeds 2 GiB", a_nrows, lda);
   if ((rc = check_tile(tile, kEpiStoreF32, N))) return rc;
   if (max_rows == 0) return EIMOE_OK;
@@ -570,6 +580,7 @@ int grouped_gemm_impl(const void* a, const int32_t* a_rows, int a_nrows, int lda
   p.max_rows = max_rows;
   p.a_rows_cap = a_nrows;
   const int epi = c_dtype == EIMOE_F32 ? kEpiStoreF32 : kEpiStoreBF16;
+  if (b_dtype == EIMOE_F32) return hip_check(launch_grouped_gemm_f32(p, epi, max_rows, tile, S(stream)), "grouped_gemm");
   return hip_check(launch_grouped_gemm(p, epi, b_dtype == EIMOE_FP8, false, max_rows, tile, S(stream)),
                    "grouped_gemm");
 }
@@ -690,8 +701,13 @@ int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int 
   if (I < 64 || I % 64) return fail(EIMOE_ERR_ALIGN, "I=%d must be a positive multiple of 64", I);
   if (shared_inter < 0 || (shared_inter > 0 && shared_inter % 64))
     return fail(EIMOE_ERR_ALIGN, "shared_inter=%d must be a multiple of 64", shared_inter);
-  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
+  if (w_dtype != EIMOE_BF16 && w_dtype != EIMOE_FP8 && w_dtype != EIMOE_F32)
+    return fail(EIMOE_ERR_DTYPE, "w_dtype=%d", w_dtype);
   if (out_dtype != EIMOE_BF16 && out_dtype != EIMOE_F32) return fail(EIMOE_ERR_DTYPE, "out_dtype=%d", out_dtype);
+  if ((w_dtype == EIMOE_F32) != ((flags & EIMOE_FP32) != 0))
+    return fail(EIMOE_ERR_DTYPE, "fp32 weights go with EIMOE_FP32 (fp32 x, h and y), and only they");
+  if ((flags & EIMOE_FP32) && (flags & (EIMOE_W8A8 | EIMOE_H_SPLIT)))
+    return fail(EIMOE_ERR_DTYPE, "EIMOE_FP32 keeps h in fp32: not with EIMOE_W8A8 or EIMOE_H_SPLIT");
   if (static_cast<long long>(T) * k > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "T*k overflows int32");
   if ((flags & EIMOE_W8A8) && w_dtype != EIMOE_FP8) return fail(EIMOE_ERR_DTYPE, "EIMOE_W8A8 needs fp8 weights");
   if ((flags & EIMOE_W8A8) && (flags & EIMOE_H_SPLIT))
@@ -700,13 +716,14 @@ int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int 
     return fail(EIMOE_ERR_ALIGN, "W8A8 needs H=%d and I=%d multiples of 128", H, I);
   {
     // The GEMMs address x, h and one expert's weights through 32-bit buffer offsets.
-    const long long wb = w_dtype == EIMOE_FP8 ? 1 : 2;
-    if (static_cast<long long>(T) * H * 2 > 0x7fffffffll)
+    const long long wb = elem_size(w_dtype);
+    const long long ab = w_dtype == EIMOE_F32 ? 4 : 2;   // x, h and shared weights
+    if (static_cast<long long>(T) * H * ab > 0x7fffffffll)
       return fail(EIMOE_ERR_SHAPE, "x (%d rows x %d) exceeds 2 GiB", T, H);
-    if (static_cast<long long>(T) * k * I * 2 > 0x7fffffffll)
+    if (static_cast<long long>(T) * k * I * ab > 0x7fffffffll)
       return fail(EIMOE_ERR_SHAPE, "h (%d x %d rows x %d) exceeds 2 GiB", T, k, I);
     if (2ll * I * H * wb > 0x7fffffffll) return fail(EIMOE_ERR_SHAPE, "one expert's gate/up weights exceed 2 GiB");
-    if (static_cast<long long>(T) * shared_inter * 2 > 0x7fffffffll || 2ll * shared_inter * H * 2 > 0x7fffffffll)
+    if (static_cast<long long>(T) * shared_inter * ab > 0x7fffffffll || 2ll * shared_inter * H * ab > 0x7fffffffll)
       return fail(EIMOE_ERR_SHAPE, "shared experts (%d rows x %d) exceed 2 GiB", T, shared_inter);
   }
   if (T == 0) return EIMOE_OK;
@@ -784,10 +801,11 @@ int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int 
       hipLaunchKernelGGL(dense_segment_kernel, dim3(1), dim3(64), 0, s2, sh_off, T);
       if ((rc = hip_check(hipGetLastError(), "shared offsets"))) return rc;
       void* sh_lo = L.h_terms == 2 ? at(L.sh_h_lo) : nullptr;
-      if ((rc = run_gate_up(x, nullptr, T, H, shared_gate_up, EIMOE_BF16, nullptr, H, shared_inter, sh_off, 1, 1, T,
+      const int sh_dtype = w_dtype == EIMOE_F32 ? EIMOE_F32 : EIMOE_BF16;   // shared weights: bf16 or fp32
+      if ((rc = run_gate_up(x, nullptr, T, H, shared_gate_up, sh_dtype, nullptr, H, shared_inter, sh_off, 1, 1, T,
                             at(L.sh_h), EIMOE_TILE_AUTO, s2, nullptr, 0, sh_lo)))
         return rc;
-      if ((rc = run_down(at(L.sh_h), shared_inter, shared_down, EIMOE_BF16, nullptr, H, sh_off, 1, 1, T, at(L.sh_y),
+      if ((rc = run_down(at(L.sh_h), shared_inter, shared_down, sh_dtype, nullptr, H, sh_off, 1, 1, T, at(L.sh_y),
                          L.y_dtype, 1, EIMOE_TILE_AUTO, s2)))
         return rc;
       if (!sh_lo) return EIMOE_OK;

@@ -166,7 +166,7 @@ struct Geo {
   static constexpr int WN = BN / WGN;
   static constexpr int MB = WM / 16;
   static constexpr int NB = WN / 16;
-  static constexpr bool SILU = (EPI == kEpiSiluBF16);
+  static constexpr bool SILU = epi_silu(EPI);
   static constexpr int NI = SILU ? NB / 2 : NB;   // adjacent output columns per lane
   static constexpr int OUT_BN = SILU ? BN / 2 : BN;
   static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile");
@@ -227,15 +227,34 @@ __device__ __forceinline__ void mma(f32x4_t (&acc)[MBE][G::NB], const bf16x8_t (
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
 }
 
-// One 64-wide K slab: two 32-wide MFMA steps, each reading its fragments first.
+// fp32 operands: a fragment's 16 bytes are 4 floats at k = 4c..4c+3 (c its chunk), one per
+// v_mfma_f32_16x16x4f32; MFMA j takes float j of every lane, so lane group q contributes k =
+// 4c+j and A and B agree on it.  Four MFMAs per fragment pair cover the 16 k of the chunk pair.
 template <class G, int MBE>
+__device__ __forceinline__ void mma_f32(f32x4_t (&acc)[MBE][G::NB], const bf16x8_t (&af)[MBE],
+                                        const bf16x8_t (&bfr)[G::NB]) {
+#pragma unroll
+  for (int i = 0; i < MBE; ++i) {
+    const f32x4_t a = __builtin_bit_cast(f32x4_t, af[i]);
+#pragma unroll
+    for (int j = 0; j < G::NB; ++j) {
+      const f32x4_t b = __builtin_bit_cast(f32x4_t, bfr[j]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q], b[q], acc[i][j], 0, 0, 0);
+    }
+  }
+}
+
+// One 64-wide K slab: two 32-wide MFMA steps, each reading its fragments first.
+template <class G, int MBE, bool F32 = false>
 __device__ __forceinline__ void slab_mma(f32x4_t (&acc)[MBE][G::NB], const uint16_t* sA, const uint16_t* sB, int wm,
                                          int wn, int lane) {
 #pragma unroll
   for (int kk = 0; kk < G::BK / 32; ++kk) {
     bf16x8_t af[MBE], bfr[G::NB];
     read_frags<G, MBE>(sA, sB, kk, wm, wn, lane, af, bfr);
-    mma<G, MBE>(acc, af, bfr);
+    if constexpr (F32) mma_f32<G, MBE>(acc, af, bfr);
+    else mma<G, MBE>(acc, af, bfr);
   }
 }
 
@@ -267,6 +286,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
           h[j] = silu_f32(g) * u;
         }
         const long long off = static_cast<long long>(row) * p.ldc + col0;
+        if constexpr (EPI == kEpiSiluF32) {
+          store_f32<G::NI>(static_cast<float*>(p.c) + off, h);
+          continue;
+        }
         store_bf16<G::NI>(static_cast<uint16_t*>(p.c) + off, h);
         if (p.c_lo) {   // the residual of the bf16 rounding, itself in bf16
 #pragma unroll
@@ -406,10 +429,13 @@ __device__ __forceinline__ void a_offsets(const GemmArgs& p, const TileCoord& tc
   }
 }
 
-// ---------------------------------------------------------------------------- bf16 weights: direct-to-LDS
-template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
+// ---------------------------------------------------------------------------- bf16 (or fp32) weights: direct-to-LDS
+// F32: fp32 A and B.  An LDS row is 128 bytes either way (64 bf16 or 32 fp32 of K per slab), so
+// the DMA, the swizzle and the fragment reads are the same bytes; only the MFMA differs.
+template <int BM, int BN, int WGM, int WGN, int EPI, int GM, bool F32 = false>
 __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmArgs p) {
   using G = Geo<BM, BN, WGM, WGN, EPI>;
+  constexpr int EB = F32 ? 4 : 2;             // bytes per element
   constexpr int BK = G::BK;
   constexpr int NW = G::NW;
   constexpr int A_PW = BM / 8 / G::NW;   // 1 KiB LDS blocks per wave per slab (8 rows each)
@@ -435,22 +461,22 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
   const long long k0 = static_cast<long long>(tc.split) * p.K;
 
   // A: lane fetches logical chunk (lane&7)^(row&7) so LDS position == swizzled position.
-  const BufRef rA{static_cast<const uint16_t*>(p.a) + k0, (p.a_rows_cap * p.lda - k0) * 2};
+  const BufRef rA{static_cast<const uint8_t*>(p.a) + k0 * EB, (p.a_rows_cap * p.lda - k0) * EB};
   uint32_t a_voff[A_PW];
-  a_offsets<A_PW, NW>(p, tc, wave, lane, 2, a_voff);
-  const uint16_t* b_base = reinterpret_cast<const uint16_t*>(expert_weights(p, tc.expert, 2)) + k0;
-  const BufRef rB{b_base, (p.b_estride - k0) * 2};
+  a_offsets<A_PW, NW>(p, tc, wave, lane, EB, a_voff);
+  const uint8_t* b_base = expert_weights(p, tc.expert, EB) + k0 * EB;
+  const BufRef rB{b_base, (p.b_estride - k0) * EB};
   uint32_t b_voff[B_PW];
 #pragma unroll
   for (int i = 0; i < B_PW; ++i) {
     const int R = (wave * B_PW + i) * 8 + lrow;
     const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
-    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb * 2 + (((lane & 7) ^ swz(R)) << 4));
+    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb * EB + (((lane & 7) ^ swz(R)) << 4));
   }
 
   const int wm = wave % WGM;
   const int wn = wave / WGM;
-  const int KT = p.K / BK;
+  const int KT = p.K * EB / (BK * 2);         // 128-byte slabs
   by_height<BM, G::MB, A_PW>(tc.row_end - tc.row0, [&]<int MBE>() {
     constexpr int A_CNT = A_PW * MBE / G::MB;
     f32x4_t acc[MBE][G::NB];
@@ -468,14 +494,14 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
     for (; kt + 1 < KT; kt += 2) {
       issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA1, sB1, wave, (kt + 1) * BK * 2);
       pin_issue();
-      slab_mma<G, MBE>(acc, sA0, sB0, wm, wn, lane);
+      slab_mma<G, MBE, F32>(acc, sA0, sB0, wm, wn, lane);
       __syncthreads();
       issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, min(kt + 2, KT - 1) * BK * 2);
       pin_issue();
-      slab_mma<G, MBE>(acc, sA1, sB1, wm, wn, lane);
+      slab_mma<G, MBE, F32>(acc, sA1, sB1, wm, wn, lane);
       __syncthreads();
     }
-    if (kt < KT) slab_mma<G, MBE>(acc, sA0, sB0, wm, wn, lane);   // odd slab count: last slab in buffer 0
+    if (kt < KT) slab_mma<G, MBE, F32>(acc, sA0, sB0, wm, wn, lane);   // odd slab count: last slab in buffer 0
     epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr);
   });
 }
@@ -774,7 +800,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8w_kernel(GemmA
 // ---------------------------------------------------------------------------- launch
 template <int BM, int BN, int WGM, int WGN, int EPI, bool BFP8, int GM>
 static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStream_t s) {
-  constexpr int OUT_BN = (EPI == kEpiSiluBF16) ? BN / 2 : BN;
+  constexpr int OUT_BN = epi_silu(EPI) ? BN / 2 : BN;
   const int n_tiles = p.N / OUT_BN;
   const long long max_mt = (static_cast<long long>(max_rows) + BM - 1) / BM + p.S;
   long long total = max_mt * n_tiles * p.k_split;
@@ -801,7 +827,7 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
 // DeepSeek-V2-Lite and Qwen3 within noise), so the layer's figure decides.
 template <int EPI, int GMX = 4>
 static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
-  constexpr int OUT_BN = (EPI == kEpiSiluBF16) ? 128 : 256;
+  constexpr int OUT_BN = epi_silu(EPI) ? 128 : 256;
   const int n_tiles = p.N / OUT_BN;
   const long long max_mt = (static_cast<long long>(max_rows) + 255) / 256 + p.S;
   long long total = max_mt * n_tiles * p.k_split;
@@ -826,7 +852,7 @@ static hipError_t launch_epi(const GemmArgs& p, int max_rows, int tile, bool a_f
 }
 
 int gemm_out_cols_per_tile(int tile, int epi) {
-  if (tile == kTileStream) return epi == kEpiSiluBF16 ? 16 : 32;   // narrowest task; wider when N allows
+  if (tile == kTileStream) return epi_silu(epi) ? 16 : 32;   // narrowest task; wider when N allows
   int bn = 0;
   switch (tile) {
     case kTileL: bn = 256; break;
@@ -835,7 +861,7 @@ int gemm_out_cols_per_tile(int tile, int epi) {
     case kTileXS: bn = 64; break;
     default: return 0;
   }
-  return epi == kEpiSiluBF16 ? bn / 2 : bn;
+  return epi_silu(epi) ? bn / 2 : bn;
 }
 
 // Tile heuristic (the host knows only the row bound, or a caller's estimate, and the shapes).
@@ -856,7 +882,7 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
   const double avg_bound = static_cast<double>(p.max_rows) / S;
   const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) / S;
   const double expert_bytes = static_cast<double>(p.nb_rows) * p.K * p.k_split * (b_fp8 ? 1 : 2);
-  const bool silu = epi == kEpiSiluBF16;
+  const bool silu = epi_silu(epi);
   int t;
   if (expert_bytes >= 32.0 * 1024 * 1024) {
     // (W8A8 gate/up at 16 rows per expert on the routed, gathered rows of a Mixtral-8x7B
@@ -904,6 +930,44 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
                                          : launch_epi<kEpiStoreBF16, false>(p, max_rows, tile, false, s);
   return b_fp8 ? launch_epi<kEpiStoreF32, true>(p, max_rows, tile, a_fp8, s)
                : launch_epi<kEpiStoreF32, false>(p, max_rows, tile, false, s);
+}
+
+template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
+static hipError_t launch_cfg_f32(const GemmArgs& p, int max_rows, hipStream_t s) {
+  constexpr int OUT_BN = epi_silu(EPI) ? BN / 2 : BN;
+  const int n_tiles = p.N / OUT_BN;
+  const long long max_mt = (static_cast<long long>(max_rows) + BM - 1) / BM + p.S;
+  long long grid = (max_mt * n_tiles * p.k_split + kNumXcd - 1) / kNumXcd * kNumXcd;
+  if (grid < kNumXcd) grid = kNumXcd;
+  if (grid > 0x7fffffffll) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((grouped_gemm_dma_kernel<BM, BN, WGM, WGN, EPI, GM, true>), dim3(static_cast<unsigned>(grid)),
+                     dim3(WGM * WGN * 64), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_epi_f32(const GemmArgs& p, int max_rows, int tile, hipStream_t s) {
+  switch (tile) {
+    case kTileM: return launch_cfg_f32<128, 128, 2, 2, EPI, 4>(p, max_rows, s);
+    case kTileS: return launch_cfg_f32<32, 128, 1, 4, EPI, 1>(p, max_rows, s);
+    case kTileXS: return launch_cfg_f32<16, 64, 1, 2, EPI, 1>(p, max_rows, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// The fp32 MFMA runs at 1/16 of the bf16 rate, so LDS and memory are far from the limit: the
+// 128x128 tile from 32 rows per segment, 32x128 and 16x64 below.
+hipError_t launch_grouped_gemm_f32(const GemmArgs& p, int epi, int max_rows, int tile, hipStream_t s) {
+  if (epi != kEpiSiluF32 && epi != kEpiStoreF32) return hipErrorInvalidValue;
+  if (tile == kTileAuto) {
+    const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) /
+                       (p.S > 0 ? p.S : 1);
+    tile = avg >= 32 ? kTileM : avg >= 12 ? kTileS : kTileXS;
+    while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) ++tile;
+  }
+  if (tile == kTileL || tile == kTileStream) tile = kTileM;
+  return epi == kEpiSiluF32 ? launch_epi_f32<kEpiSiluF32>(p, max_rows, tile, s)
+                            : launch_epi_f32<kEpiStoreF32>(p, max_rows, tile, s);
 }
 
 }  // namespace eimoe

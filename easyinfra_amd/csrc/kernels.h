@@ -8,7 +8,8 @@ namespace eimoe {
 
 constexpr int kMaxSeg = 1024;  // segments (local experts x source ranks) per grouped GEMM
 
-enum Epilogue : int { kEpiStoreF32 = 0, kEpiStoreBF16 = 1, kEpiSiluBF16 = 2 };
+enum Epilogue : int { kEpiStoreF32 = 0, kEpiStoreBF16 = 1, kEpiSiluBF16 = 2, kEpiSiluF32 = 3 };
+constexpr bool epi_silu(int epi) { return epi == kEpiSiluBF16 || epi == kEpiSiluF32; }
 
 // One grouped GEMM launch: for each segment s (rows [seg_off[s], seg_off[s+1]) of A),
 // C[rows, :] = A[rows, :] . B[s % e_mod]^T  (B in nn.Linear layout [N_b, K]).
@@ -112,6 +113,9 @@ bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8);
 int stream_out_cols(int N, int epi, bool fp8);   // widest output columns per streaming task (0: unsupported)
 hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s);
 int gemm_out_cols_per_tile(int tile, int epi);
+// fp32 operands on the fp32 MFMA (v_mfma_f32_16x16x4f32): A, B and the output in fp32 (epi
+// kEpiSiluF32 or kEpiStoreF32); LDS-tiled kernels only (tiles 128x128, 32x128, 16x64).
+hipError_t launch_grouped_gemm_f32(const GemmArgs& p, int epi, int max_rows, int tile, hipStream_t s);
 
 // Base of expert e's weights: the pointer table when given, else b + e * b_estride elements.
 __device__ __forceinline__ const uint8_t* expert_weights(const GemmArgs& p, int e, int elem_bytes) {

@@ -219,9 +219,11 @@ def gather(x: torch.Tensor, rows: torch.Tensor, num_rows: torch.Tensor, max_rows
 def gemm_gate_up_silu(a: torch.Tensor, w_gate_up: torch.Tensor, seg_offsets: torch.Tensor, max_rows: int,
                       a_rows: Optional[torch.Tensor] = None, w_scale: Optional[torch.Tensor] = None,
                       e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
-    """fused_moe.py:445-459: h = silu(a.Wg^T) * (a.Wu^T) per segment -> bf16 [max_rows, I]."""
-    _req(a, "a", torch.bfloat16, 2)
-    _req(w_gate_up, "w_gate_up", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    """fused_moe.py:445-459: h = silu(a.Wg^T) * (a.Wu^T) per segment -> bf16 [max_rows, I]
+    (fp32 a and weights: the fp32 MFMA, fp32 h)."""
+    f32 = w_gate_up.dtype == torch.float32
+    _req(a, "a", torch.float32 if f32 else torch.bfloat16, 2)
+    _req(w_gate_up, "w_gate_up", (torch.bfloat16, torch.float8_e4m3fn, torch.float32), 3)
     _req(seg_offsets, "seg_offsets", torch.int32, 1)
     E, I2, H = w_gate_up.shape
     I = I2 // 2
@@ -236,7 +238,7 @@ def gemm_gate_up_silu(a: torch.Tensor, w_gate_up: torch.Tensor, seg_offsets: tor
         raise ValueError("fp8 weights need w_scale [E, 2I]; bf16 weights take none")
     if w_scale is not None:
         _req_shape(w_scale, "w_scale", (E, I2))
-    h = torch.empty(max_rows, I, dtype=torch.bfloat16, device=a.device)
+    h = torch.empty(max_rows, I, dtype=torch.float32 if f32 else torch.bfloat16, device=a.device)
     call("eimoe_gemm_gate_up_silu", a.data_ptr(), _ptr(a_rows), a.shape[0], a.stride(0), w_gate_up.data_ptr(),
          _dt(w_gate_up),
          _ptr(w_scale), H, I, seg_offsets.data_ptr(), seg_offsets.numel() - 1, e_mod or E, max_rows, h.data_ptr(),
@@ -247,9 +249,13 @@ def gemm_gate_up_silu(a: torch.Tensor, w_gate_up: torch.Tensor, seg_offsets: tor
 def gemm_down(h: torch.Tensor, w_down: torch.Tensor, seg_offsets: torch.Tensor, max_rows: int,
               out_dtype=torch.float32, k_split: int = 1, w_scale: Optional[torch.Tensor] = None,
               e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
-    """fused_moe.py:463-476: y = h . Wd^T per segment -> [k_split, max_rows, H] partial planes."""
-    _req(h, "h", torch.bfloat16, 2)
-    _req(w_down, "w_down", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    """fused_moe.py:463-476: y = h . Wd^T per segment -> [k_split, max_rows, H] partial planes
+    (fp32 h and weights: the fp32 MFMA, fp32 y)."""
+    f32 = w_down.dtype == torch.float32
+    _req(h, "h", torch.float32 if f32 else torch.bfloat16, 2)
+    _req(w_down, "w_down", (torch.bfloat16, torch.float8_e4m3fn, torch.float32), 3)
+    if f32 and out_dtype != torch.float32:
+        raise TypeError("fp32 weights write fp32 y")
     _req(seg_offsets, "seg_offsets", torch.int32, 1)
     E, H, I = w_down.shape
     if h.shape[1] != I:
@@ -320,9 +326,13 @@ def gemm_down_w8a8(hq: torch.Tensor, h_scale: torch.Tensor, w_down: torch.Tensor
 def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg_offsets: torch.Tensor, max_rows: int,
                  out_dtype=torch.bfloat16, a_rows: Optional[torch.Tensor] = None,
                  b_scale: Optional[torch.Tensor] = None, e_mod: Optional[int] = None, tile: int = 0) -> torch.Tensor:
-    """single_group_gemm_moe.py:76-91: c[rows_s] = a[rows_s] . b[s % e_mod]^T, b packed [E,N,K]."""
-    _req(a, "a", torch.bfloat16, 2)
-    _req(b, "b", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    """single_group_gemm_moe.py:76-91: c[rows_s] = a[rows_s] . b[s % e_mod]^T, b packed [E,N,K]
+    (fp32 a and b: the fp32 MFMA, fp32 c)."""
+    f32 = b.dtype == torch.float32
+    _req(a, "a", torch.float32 if f32 else torch.bfloat16, 2)
+    _req(b, "b", (torch.bfloat16, torch.float8_e4m3fn, torch.float32), 3)
+    if f32:
+        out_dtype = torch.float32
     _req(seg_offsets, "seg_offsets", torch.int32, 1)
     E, N, K = b.shape
     if a.shape[1] != K:
@@ -409,7 +419,9 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     ``w_scales=(s_gate_up [E,2I], s_down [E,H])`` marks fp8-e4m3 weights: bf16 activations on
     the bf16 MFMA (W8A16), or with ``w8a8=True`` activations quantised per token / per row
     and both GEMMs on the fp8 MFMA (W8A8).
-    fp32 hidden states are rounded to bf16 for the MFMA path.
+    fp32 hidden states with fp32 weights run the fp32 layer (fp32 MFMA, fp32 h and y: the
+    reference's fp32 F.linear path, native_moe.py:56-103); fp32 hidden states with bf16 or fp8
+    weights are refused rather than rounded.
     ``h_split=True`` is the precise mode: h = silu(g)*u is kept as a pair of bf16 terms (hi + lo)
     and the down projection runs once per term, so h carries ~16 significant bits instead of 8
     (twice the down projection's time; per-assignment outputs in fp32).
@@ -420,9 +432,11 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     ``num_experts`` giving E when it is not the top of ``expert_range``).
     """
     x = hidden_states
-    if x.dtype == torch.float32:
-        x = x.to(torch.bfloat16)
-    _req(x, "hidden_states", torch.bfloat16, 2)
+    f32 = w_gate_up.dtype == torch.float32
+    if x.dtype == torch.float32 and not f32:
+        raise TypeError("fp32 hidden_states need fp32 weights (the fp32 layer); cast the hidden states to bf16 "
+                        "explicitly to run them on bf16 or fp8 weights")
+    _req(x, "hidden_states", torch.float32 if f32 else torch.bfloat16, 2)
     if scoring_func not in ("softmax", "sigmoid"):
         raise ValueError(f"scoring_func {scoring_func!r}: 'softmax' or 'sigmoid'")
     if scoring_func == "sigmoid" and routing is None:
@@ -430,8 +444,8 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
                                       renormalize, routed_scaling_factor)
     if routing is None or router_logits is not None:
         _req(router_logits, "router_logits", torch.float32, 2)
-    _req(w_gate_up, "w_gate_up", (torch.bfloat16, torch.float8_e4m3fn), 3)
-    _req(w_down, "w_down", (torch.bfloat16, torch.float8_e4m3fn), 3)
+    _req(w_gate_up, "w_gate_up", (torch.bfloat16, torch.float8_e4m3fn, torch.float32), 3)
+    _req(w_down, "w_down", (w_gate_up.dtype, torch.float8_e4m3fn) if not f32 else torch.float32, 3)
     T, H = x.shape
     n_local, I2, H2 = w_gate_up.shape
     if router_logits is not None:
@@ -455,16 +469,21 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     if (shared_gate_up is None) != (shared_down is None):
         raise ValueError("shared experts need both shared_gate_up [2*Is, H] and shared_down [H, Is]")
     if shared_gate_up is not None:
-        _req(shared_down, "shared_down", torch.bfloat16, 2)
+        sh_dt = torch.float32 if f32 else torch.bfloat16
+        _req(shared_down, "shared_down", sh_dt, 2)
         Is = shared_down.shape[1]
-        _req_shape(shared_gate_up, "shared_gate_up", (2 * Is, H), torch.bfloat16)
-        _req_shape(shared_down, "shared_down", (H, Is), torch.bfloat16)
+        _req_shape(shared_gate_up, "shared_gate_up", (2 * Is, H), sh_dt)
+        _req_shape(shared_down, "shared_down", (H, Is), sh_dt)
     if w8a8 and not fp8:
         raise ValueError("w8a8 needs fp8 weights and w_scales")
     if w8a8 and h_split:
         raise ValueError("h_split keeps h as bf16 terms; w8a8 quantises it to fp8")
     flags = (_lib.RENORMALIZE if renormalize else 0) | (_lib.Y_F32 if y_fp32 else 0) | (_lib.W8A8 if w8a8 else 0)
     flags |= _lib.H_SPLIT if h_split else 0
+    if f32:
+        if w8a8 or h_split:
+            raise ValueError("the fp32 layer keeps h in fp32: no w8a8 or h_split")
+        flags |= _lib.FP32
     if routing is not None:
         ids_in, w_in = routing
         _req(ids_in, "routing ids", torch.int32, 2)

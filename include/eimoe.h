@@ -48,9 +48,13 @@ enum {
   EIMOE_W8A8 = 4,        /* fp8 weights: also quantise activations per token and run the fp8 MFMA */
   EIMOE_ROUTING_IN = 8,  /* topk_ids / topk_w are inputs (routing done by the caller, e.g. with
                             eimoe_router_grouped_topk); logits are not read and may be NULL */
-  EIMOE_H_SPLIT = 16     /* precise mode: the SiLU*mul intermediate h is kept as two bf16 terms
+  EIMOE_H_SPLIT = 16,    /* precise mode: the SiLU*mul intermediate h is kept as two bf16 terms
                             (h = hi + lo, ~16 significant bits instead of 8) and the down projection
                             runs once per term (twice its time); y is kept in fp32.  Not with W8A8. */
+  EIMOE_FP32 = 32        /* fp32 layer: x, the weights (w_dtype EIMOE_F32, shared weights too), h
+                            and y in fp32 on the fp32 MFMA (the reference's fp32 F.linear path,
+                            native_moe.py:56-103).  Required with, and only with, fp32 weights;
+                            size the workspace with it.  Not with W8A8 or H_SPLIT. */
 };
 
 /* tile selector for the GEMM entry points (0 = automatic).  EIMOE_TILE_STREAM is the
@@ -139,13 +143,15 @@ int eimoe_gather(const void* x, int dtype, int H, const int32_t* rows, const int
  * directly; every a_rows entry must be < a_nrows, reads beyond the buffer return 0).
  * w_gate_up: [E_w, 2I, H] bf16 or fp8 (rows [0,I) gate, [I,2I) up, fused_moe.py:91-101);
  * w_scale: fp8 only, [E_w, 2I] fp32 per-output-channel scales.  h: bf16 [max_rows, I].
+ * w_dtype EIMOE_F32: a and w_gate_up fp32 on the fp32 MFMA, h fp32 [max_rows, I].
  * H % 64 == 0, I % 32 == 0.  max_rows bounds seg_offsets[n_seg]. */
 int eimoe_gemm_gate_up_silu(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* w_gate_up, int w_dtype,
                             const float* w_scale, int H, int I, const int32_t* seg_offsets, int n_seg, int e_mod,
                             int max_rows, void* h, int tile, void* stream);
 
 /* Grouped down GEMM: y[r,:] = h[r,:] . W_d[e]^T (fused_moe.py:463-476).
- * h: bf16 [max_rows, I]; w_down: [E_w, H, I] bf16 or fp8 (+ w_scale [E_w, H]).
+ * h: bf16 [max_rows, I]; w_down: [E_w, H, I] bf16 or fp8 (+ w_scale [E_w, H]); or h and w_down
+ * fp32 with w_dtype EIMOE_F32 (the fp32 MFMA; y_dtype EIMOE_F32).
  * y: y_dtype (EIMOE_F32 / EIMOE_BF16) [k_split][max_rows, H]; with k_split > 1 each K-slice
  * writes its own partial plane (summed by eimoe_combine), I/k_split % 64 == 0. */
 int eimoe_gemm_down(const void* h, int I, const void* w_down, int w_dtype, const float* w_scale, int H,
@@ -170,7 +176,7 @@ int eimoe_gemm_down_w8a8(const void* hq, const float* h_scale, int I, const void
 /* Plain grouped GEMM, the X_grouped_gemm_single(A, B_list, block_sizes) contract
  * (single_group_gemm_moe.py:76-91): c[rows_s] = a[rows_s] . B[s % e_mod]^T with B packed as
  * [E_w, N, K] (b_expert_stride elements apart).  a bf16 [a_nrows, lda] (rows gathered through a_rows
- * when given); b bf16/fp8 (+b_scale [E_w,N]);
+ * when given); b bf16/fp8 (+b_scale [E_w,N]), or a and b fp32 with b_dtype EIMOE_F32 (c fp32);
  * c f32 or bf16 [max_rows, N].  K % 64 == 0, N % 64 == 0. */
 int eimoe_grouped_gemm(const void* a, const int32_t* a_rows, int a_nrows, int lda, const void* b, int b_dtype,
                        const float* b_scale, long long b_expert_stride, int N, int K, const int32_t* seg_offsets,
@@ -233,6 +239,7 @@ size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_
  *   (bf16 or fp8 with per-channel scales [n_local,2I] / [n_local,H]); experts e_lo..e_lo+n_local-1
  *   of the router's E are resident (pass 0, E for a whole layer); shared experts optional
  *   (shared_gate_up [2*Is,H], shared_down [H,Is] bf16, weight 1.0); out [T,H] in out_dtype.
+ *   With EIMOE_FP32: x, the weights (w_dtype EIMOE_F32) and the shared weights are fp32.
  * Optional outputs (may be NULL): topk_ids_out [T,k] int32, topk_w_out [T,k] fp32; with
  * EIMOE_ROUTING_IN both are required inputs instead and the router is skipped. */
 int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int E, int k, const void* w_gate_up,

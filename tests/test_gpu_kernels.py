@@ -499,3 +499,34 @@ def test_fp8_gemms_remainder_tile_heights(dev, tile):
         torch.testing.assert_close(y8[a:b], (hq[a:b].float() @ qd[e].float().T) * sh[a:b][:, None] * sd[e][None, :],
                                    rtol=1e-4, atol=1e-4)
         torch.testing.assert_close(y16[a:b], (h16[a:b] @ qd[e].float().T) * sd[e][None, :], rtol=1e-3, atol=1e-3)
+
+
+# fp32 operands on the fp32 MFMA (the fp32 layer): every LDS tile, remainder heights of the 128x128
+# tile, K split planes; against float64 with only the summation order left to differ.
+@pytest.mark.parametrize("tile", [0, 2, 3, 4])
+@pytest.mark.parametrize("k_split", [1, 2])
+def test_fp32_gemms(dev, tile, k_split):
+    counts = [33, 0, 64, 65, 129, 7, 300]
+    g = torch.Generator().manual_seed(5 + tile + k_split)
+    H, I = 256, 128
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 90
+    x = torch.randn(T, H, generator=g)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
+    wgu = torch.randn(E, 2 * I, H, generator=g) * 0.05
+    wd = torch.randn(E, H, I, generator=g) * 0.05
+    h = ops.gemm_gate_up_silu(x.to(dev), wgu.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev), tile=tile)
+    assert h.dtype == torch.float32
+    y = cpu(ops.gemm_down(h, wd.to(dev), off_t.to(dev), rows, out_dtype=torch.float32, k_split=k_split,
+                          tile=tile)).sum(0).double()
+    h = cpu(h).double()
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        gu = x[a_rows[a:b].long()].double() @ wgu[e].double().T
+        href = gu[:, :I] * torch.sigmoid(gu[:, :I]) * gu[:, I:]
+        torch.testing.assert_close(h[a:b], href, rtol=2e-5, atol=2e-6)
+        torch.testing.assert_close(y[a:b], h[a:b] @ wd[e].double().T, rtol=2e-5, atol=2e-6)

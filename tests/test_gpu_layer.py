@@ -25,10 +25,9 @@ def cpu(t):
 
 
 def _run(inp, dev, out_dtype=torch.float32, **kw):
+    """The fused layer on the workload's own dtypes (fp32 workloads run the fp32 layer)."""
     s = inp.shape
     wgu, wd = inp.w_gate_up, inp.w_down
-    if wgu.dtype == torch.float32:
-        wgu, wd = wgu.to(torch.bfloat16), wd.to(torch.bfloat16)
     sh_gu = inp.shared_gate_up.to(dev) if inp.shared_gate_up is not None else None
     sh_d = inp.shared_down.to(dev) if inp.shared_down is not None else None
     return ops.fused_moe(inp.x.to(dev), inp.logits.to(dev), s.top_k, wgu.to(dev), wd.to(dev),
@@ -57,12 +56,13 @@ def test_layer_small_variant(dev, name, T):
     got = cpu(out)
     ref = _oracle(inp)
     tight = _oracle(inp, round_h=True)
-    # fp32 inputs (the tiny-mixtral-fp32 workload) are rounded to bf16 for MFMA.
-    xin = inp.x if inp.x.dtype == torch.bfloat16 else inp.x.to(torch.bfloat16).float()
     assert oracle.rel_l2(got, ref) <= 1e-2
     assert float((got - ref).abs().max()) <= 2e-2
     if inp.x.dtype == torch.bfloat16:
         assert float((got - tight).abs().max()) <= 2e-3 * max(1.0, float(tight.abs().max()))
+    else:   # the fp32 layer: fp32 operands on the fp32 MFMA, only the summation order differs
+        assert oracle.rel_l2(got, ref) <= 2e-5
+        assert float((got - ref).abs().max()) <= 1e-4 * max(1.0, float(ref.abs().max()))
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
@@ -174,9 +174,11 @@ def test_layer_real_shape(dev, name, T):
     assert torch.equal(cpu(ids), rid)
     ref = _oracle(inp.to("cpu"))
     got = cpu(out)
+    f32 = inp.x.dtype == torch.float32      # the fp32 layer: h is fp32 already, no precise mode
+    precise = {} if f32 else {"h_split": True}
     got16 = cpu(_run(inp, dev, out_dtype=torch.bfloat16)[0]).float()
-    gotp = cpu(_run(inp, dev, h_split=True)[0])
-    gotp16 = cpu(_run(inp, dev, out_dtype=torch.bfloat16, h_split=True)[0]).float()
+    gotp = cpu(_run(inp, dev, **precise)[0])
+    gotp16 = cpu(_run(inp, dev, out_dtype=torch.bfloat16, **precise)[0]).float()
 
     def err(a):
         return oracle.rel_l2(a, ref), float((a - ref).abs().max())
@@ -193,6 +195,8 @@ def test_layer_real_shape(dev, name, T):
     assert rel <= 1e-2 and rel16 <= 1e-2
     assert relp <= 1e-2 and mxp <= 2e-2
     assert relp16 <= 1e-2 and excessp16 <= 2e-2
+    if f32:   # the reference's own precision: fp32 operands, only the summation order differs
+        assert rel <= 2e-5 and mx <= 1e-4 * max(1.0, float(ref.abs().max()))
 
 
 @pytest.mark.parametrize("name", ["mixtral-8x7b", "deepseek-v2-lite", "qwen3-30b-a3b-local32"])
@@ -234,6 +238,14 @@ def test_block_prologue_then_v3_layer(dev):
     ids, w = oracle.route_grouped_topk(cpu(logits), k, 8, 4, bias, True, 2.5)
     ref = oracle.moe_forward(cpu(normed), cpu(logits), k, wgu, wd, True, sg, sd, routing=(ids, w))
     assert oracle.rel_l2(cpu(out), ref) <= 1e-2
+
+
+def test_fp32_hidden_states_on_bf16_weights_are_refused(dev):
+    """fp32 activations run the fp32 layer with fp32 weights; on bf16 weights they are refused
+    rather than rounded silently."""
+    inp = make_inputs(SHAPES["mixtral-8x7b"], 4, device="cpu", hidden=256, inter=128)
+    with pytest.raises(TypeError):
+        ops.fused_moe(inp.x.float().to(dev), inp.logits.to(dev), 2, inp.w_gate_up.to(dev), inp.w_down.to(dev))
 
 
 def test_fused_moe_refuses_mis_shaped_scales_and_shared_weights(dev):
