@@ -514,8 +514,10 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
 // DMA), so each SIMD's MFMA pipe is fed by one wave while the other waits on LDS.  A phase
 // is half a slab (32-wide K) and ends with a workgroup barrier; group 1 enters one phase late
 // and group 0 adds one barrier at the end, so both groups execute 4*KT + 2 of them.  Same
-// tiles, LDS layout, DMA and accumulation order as grouped_gemm_dma_kernel<256, 256, 4, 2>:
-// bit-identical results, 3-4 % faster on the Mixtral-8x7B prefill GEMMs (MI355X).
+// tiles, LDS layout and accumulation order as grouped_gemm_dma_kernel<256, 256, 4, 2>:
+// bit-identical results, 3-4 % faster on the Mixtral-8x7B prefill GEMMs (MI355X) with two B
+// stages; the third B stage below gains another 1-4 % there (A/B on one box: gate/up 3.31 ->
+// 3.28 ms, down with K split 2 1.685 -> 1.645 ms, DeepSeek-V2-Lite 1-2 %).
 // Workgroup barrier without a memory fence: a fence would wait for the DMA still in flight
 // (it writes LDS).  The callers wait for what must be complete (lgkmcnt for their fragment
 // reads, vmcnt for their DMA) explicitly; the asm's memory clobber keeps the compiler from
@@ -528,21 +530,50 @@ __device__ __forceinline__ void pp_barrier() {
 __device__ __forceinline__ void pp_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }     // vmcnt(0)
 __device__ __forceinline__ void pp_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }   // lgkmcnt(0)
 
+// ---------------------------------------------------------------------------- bf16 ping-pong, three B stages
+// The ping-pong kernel with the weight panel (B, the operand streamed from HBM) fetched two slabs
+// ahead: A in two stages, B in three, 5 x 32 KiB = the whole 160 KiB of LDS (the segment prefix
+// lives in the third B stage until that stage's first load).  At the top of slab kt every wave
+// issues A(kt+1) then B(kt+2); the slab ends waiting for all but the last B_PW loads of the wave
+// (vmcnt(4): loads complete in issue order), so A(kt+1) and B(kt+1) have landed and B(kt+2) may
+// still be in flight.  Unrolled by six so every stage index is static.
+__device__ __forceinline__ void pp_wait_vm4() { __builtin_amdgcn_s_waitcnt(0x0F74); }   // vmcnt(4)
+
+template <int A_CNT, int B_PW, int NW, int A_PW>
+__device__ __forceinline__ void issue_ab_dma(const BufRef& a, const BufRef& b, const uint32_t (&a_voff)[A_PW],
+                                             const uint32_t (&b_voff)[B_PW], uint16_t* sA, uint16_t* sB, int wave,
+                                             int soff_a, int soff_b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto rA = make_rsrc(a.base, a.bytes);
+  const auto rB = make_rsrc(b.base, b.bytes);
+#pragma unroll
+  for (int i = 0; i < A_CNT; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void_t*)(sA + (i * NW + wave) * 512), 16, a_voff[i], soff_a,
+                                             0, 0);
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_void_t*)(sB + (wave * B_PW + i) * 512), 16, b_voff[i], soff_b,
+                                             0, 0);
+#endif
+}
+
 template <int EPI, int GM>
-__global__ void __launch_bounds__(512) grouped_gemm_pp_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
   using G = Geo<256, 256, 4, 2, EPI>;
   constexpr int BK = G::BK;
   constexpr int NW = G::NW;
-  constexpr int A_PW = 256 / 8 / G::NW;   // 1 KiB LDS blocks per wave per slab
+  constexpr int A_PW = 256 / 8 / G::NW;
   constexpr int B_PW = 256 / 8 / G::NW;
+  static_assert(B_PW == 4, "the slab-end wait is vmcnt(B_PW)");
+  static_assert((kMaxSeg + 1) * sizeof(int) <= 256 * BK * sizeof(uint16_t), "segment prefix fits a B stage");
   __shared__ __attribute__((aligned(1024))) uint16_t sA0[256 * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sA1[256 * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sB0[256 * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sB1[256 * BK];
-  __shared__ int s_pref[kMaxSeg + 1];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB2[256 * BK];
 
   TileCoord tc;
-  if (!decode_tile<256, G::OUT_BN, GM>(p, s_pref, tc)) return;
+  if (!decode_tile<256, G::OUT_BN, GM>(p, reinterpret_cast<int*>(sB2), tc)) return;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -574,40 +605,43 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, 0);
+    // slab 0 into (A0, B0), B of slab 1 into B1 (the prefix in B2 is no longer read: every
+    // thread finished decode_tile before the barrier below, and B2's first load comes after it)
+    issue_ab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, 0, 0);
+    issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
     pp_wait_vm0();
     pp_barrier();
     if (grp == 1) pp_barrier();
-    // One phase pair per 32-wide half slab: read the half's fragments, barrier, multiply,
-    // barrier.  Every wave issues its share of the next slab with its first half (group 1
-    // one phase after group 0); group 1 waits for it at the end of its second read phase,
-    // group 0 at the end of its second multiply phase: both before the barrier after which
-    // group 0 reads that slab.
     bf16x8_t af[MBE], bfr[G::NB];
-#define EIMOE_PP_HALF(SA, SB, KK)                         \
+#define EIMOE_PP3_HALF(SA, SB, KK)                         \
     read_frags<G, MBE>(SA, SB, KK, wm, wn, lane, af, bfr); \
     pp_wait_lgkm0();                                       \
-    if (KK == 1 && grp == 1) pp_wait_vm0();                \
+    if (KK == 1 && grp == 1) pp_wait_vm4();                \
     pp_barrier();                                          \
     mma<G, MBE>(acc, af, bfr);                             \
-    if (KK == 1 && grp == 0) pp_wait_vm0();                \
+    if (KK == 1 && grp == 0) pp_wait_vm4();                \
     pp_barrier();
-    int kt = 0;
-    for (; kt + 1 < KT; kt += 2) {
-      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA1, sB1, wave, (kt + 1) * BK * 2);
-      EIMOE_PP_HALF(sA0, sB0, 0)
-      EIMOE_PP_HALF(sA0, sB0, 1)
-      // the last pair re-reads slab KT-1 into buffer 0 (not read again), keeping the loop branch-free
-      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, min(kt + 2, KT - 1) * BK * 2);
-      EIMOE_PP_HALF(sA1, sB1, 0)
-      EIMOE_PP_HALF(sA1, sB1, 1)
+    // slab kt + J: read (SA, SB); load A(kt+J+1) into SAN and B(kt+J+2) into SBN (clamped to
+    // the last slab near the end: those stages are not read again)
+#define EIMOE_PP3_SLAB(J, SA, SB, SAN, SBN)                                                              \
+    if (kt + J < KT) {                                                                                   \
+      issue_ab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, min(kt + J + 1, KT - 1) * BK * 2, \
+                                    min(kt + J + 2, KT - 1) * BK * 2);                                   \
+      EIMOE_PP3_HALF(SA, SB, 0)                                                                          \
+      EIMOE_PP3_HALF(SA, SB, 1)                                                                          \
     }
-    if (kt < KT) {   // odd slab count: the last slab is in buffer 0
-      EIMOE_PP_HALF(sA0, sB0, 0)
-      EIMOE_PP_HALF(sA0, sB0, 1)
+    for (int kt = 0; kt < KT; kt += 6) {
+      EIMOE_PP3_SLAB(0, sA0, sB0, sA1, sB2)
+      EIMOE_PP3_SLAB(1, sA1, sB1, sA0, sB0)
+      EIMOE_PP3_SLAB(2, sA0, sB2, sA1, sB1)
+      EIMOE_PP3_SLAB(3, sA1, sB0, sA0, sB2)
+      EIMOE_PP3_SLAB(4, sA0, sB1, sA1, sB0)
+      EIMOE_PP3_SLAB(5, sA1, sB2, sA0, sB1)
     }
-#undef EIMOE_PP_HALF
+#undef EIMOE_PP3_SLAB
+#undef EIMOE_PP3_HALF
     if (grp == 0) pp_barrier();   // matches group 1's late start
+    pp_wait_vm0();                // the clamped loads near the end land before the LDS is released
     epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr);
   });
 }
@@ -834,7 +868,7 @@ static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
   long long grid = (total + kNumXcd - 1) / kNumXcd * kNumXcd;
   if (grid < kNumXcd) grid = kNumXcd;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((grouped_gemm_pp_kernel<EPI, GMX>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, s, p);
+  hipLaunchKernelGGL((grouped_gemm_pp3_kernel<EPI, GMX>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, s, p);
   return hipGetLastError();
 }
 
