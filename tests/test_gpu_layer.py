@@ -274,3 +274,20 @@ def test_fused_moe_refuses_mis_shaped_scales_and_shared_weights(dev):
     with pytest.raises(ValueError):
         ops.gemm_gate_up_silu(x, qgu, off, 8, w_scale=sgu[:1].contiguous())
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("name,T", [("qwen3-30b-a3b-local32", 200), ("qwen3-30b-a3b-local32", 600),
+                                    ("qwen3-30b-a3b-local32", 3000), ("deepseek-v2-lite", 700),
+                                    ("mixtral-8x7b", 500), ("mixtral-8x7b", 2900)])
+def test_layer_routing_paths(dev, name, T):
+    """Batch sizes that take each routing path of the fused layer: the one-workgroup router + align
+    (up to 2 routing steps), the router then the one-workgroup align, and the router then the
+    many-workgroup align (from 4096 routed pairs: several chunks, a ragged last one).  Ids
+    bit-exact, output against the oracle."""
+    inp = make_inputs(SHAPES[name], T, device="cpu", hidden=128, inter=64)
+    out, ids, w = _run(inp, dev)
+    rid, rw = oracle.route_topk(inp.logits, inp.shape.top_k, inp.shape.renormalize)
+    assert torch.equal(cpu(ids), rid)
+    torch.testing.assert_close(cpu(w), rw, rtol=3e-6, atol=1e-7)
+    ref = _oracle(inp, round_h=True)
+    assert float((cpu(out) - ref).abs().max()) <= 2e-3 * max(1.0, float(ref.abs().max()))
