@@ -767,6 +767,16 @@ int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int 
   const hipStream_t s = S(stream);
   const int A = T * k;
   int rc;
+  // A decode step of a few routed pairs on small experts (T*k <= 16 and <= E/2, at most 4 MiB of
+  // down weights per expert): the down projection and the combine as one kernel per (token,
+  // column block).  Measured against the streaming down projection + combine (one box): the
+  // Qwen3-30B-A3B 32-expert share (3 MiB experts) at 1 and 2 tokens 26.5 -> 22.1 and 22.0 ->
+  // 17.6 us; slower at 8 tokens (47 -> 50 us) and on larger experts (DeepSeek-V2-Lite, 5.8 MiB,
+  // 1 token: 74 -> 83 us; Mixtral-8x7B): a plain-FMA GEMV streams them below the MFMA streaming
+  // kernel's rate.
+  const bool down_combine = !(flags & (EIMOE_W8A8 | EIMOE_FP32)) && w_dtype == EIMOE_BF16 &&
+                            down_combine_supported(H, I) && A <= 16 && 2ll * A <= E &&
+                            static_cast<long long>(H) * I * 2 <= 4ll * 1024 * 1024;
   // Routing first: the shared experts forked below would otherwise fill the GPU ahead of the small
   // routing kernels on the critical path.
   if (routing_in) {
@@ -847,6 +857,7 @@ int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int 
       if ((rc = run_gate_up(x, sorted_tok, T, H, w_gate_up, w_dtype, w_gate_up_scale, H, I, offsets, n_local, n_local,
                             A, at(L.h), EIMOE_TILE_AUTO, s, nullptr, L.rows_hint, h_lo)))
         return rc;
+      if (down_combine) return EIMOE_OK;   // projected inside the combine below
       if ((rc = run_down(at(L.h), I, w_down, w_dtype, w_down_scale, H, offsets, n_local, n_local, A, at(L.y),
                          L.y_dtype, L.k_split, EIMOE_TILE_AUTO, s, nullptr, L.rows_hint)))
         return rc;
@@ -864,6 +875,10 @@ int fused_moe_impl(const void* x, const float* logits, int T, int H, int I, int 
     if (!rc) rc = rj;
   }
   if (rc) return rc;
+  if (down_combine)
+    return hip_check(launch_down_combine(at(L.h), L.h_terms == 2 ? at(L.h_lo) : nullptr, w_down, I, H, ids, w, pos, T,
+                                         k, e_lo, sh_y, L.y_dtype, L.h_terms, out, out_dtype, s),
+                     "down + combine");
   return hip_check(launch_combine(at(L.y), L.y_dtype, L.h_terms * L.k_split, static_cast<long long>(A) * H, pos, w, T,
                                   k, H, sh_y, L.y_dtype, L.h_terms, out, out_dtype, s),
                    "combine");

@@ -100,6 +100,12 @@ hipError_t launch_gather_rows(const void* x, int row_bytes, const int32_t* rows,
 hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long split_stride, const int32_t* pos,
                           const float* w, int T, int k, int H, const void* shared_y, int shared_dtype, int shared_n,
                           void* out, int out_dtype, hipStream_t s);
+// Decode: the down projection and the weighted combine in one kernel, per (token, 16 output
+// columns), for bf16 weights [n_local][H][I] and bf16 h rows found through pos (h_lo optional).
+bool down_combine_supported(int H, int I);
+hipError_t launch_down_combine(const void* h, const void* h_lo, const void* w_down, int I, int H, const int32_t* ids,
+                               const float* w, const int32_t* pos, int T, int k, int e_lo, const void* shared_y,
+                               int shared_dtype, int shared_n, void* out, int out_dtype, hipStream_t s);
 // epi: Epilogue; b_fp8: B is e4m3; max_rows bounds the grid; tile: TileCfg.
 // a_fp8: A and B are both fp8-e4m3 (W8A8 on the fp8 MFMA); b_fp8 alone: W8A16.
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,

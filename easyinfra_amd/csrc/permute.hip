@@ -135,4 +135,88 @@ hipError_t launch_combine(const void* y, int y_dtype, int n_split, long long spl
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------- decode: down + combine
+// For a few routed pairs per expert (a decode step where each resident expert serves about one
+// token) the down projection and the weighted combine run as one kernel, per (token, block of
+// kDcCols output columns): for each of the token's slots in slot order whose expert is resident,
+// y = h[pos] . W_d[e][cols]^T (h = hi + lo when the precise mode keeps a second term), then
+// out[t, cols] = sum_j w_j * y_j (+ the shared-expert planes), fp32 throughout.  No y round trip
+// through memory and no combine launch.  The 256 threads are kDcCols columns x kDcSlices K slices;
+// each slice's partial sums are added in slice order through LDS (deterministic).
+constexpr int kDcCols = 16;
+constexpr int kDcSlices = 16;
+
+__global__ __launch_bounds__(kDcCols* kDcSlices) void down_combine_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ h_lo, const uint16_t* __restrict__ w_down, int I,
+    int H, const int32_t* __restrict__ ids, const float* __restrict__ wts, const int32_t* __restrict__ pos, int k,
+    int e_lo, const void* __restrict__ shared_y, int shared_dtype, int shared_n, int T, void* __restrict__ out,
+    int out_dtype) {
+  __shared__ float part[kDcSlices][kDcCols];
+  const int c = threadIdx.x % kDcCols;
+  const int q = threadIdx.x / kDcCols;
+  const int t = blockIdx.y;
+  const int col = blockIdx.x * kDcCols + c;
+  const int per = I / kDcSlices;          // a multiple of 8
+  const int k0 = q * per;
+  float acc = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const int p = pos[static_cast<long long>(t) * k + j];
+    if (p < 0) continue;                  // expert not resident on this GPU
+    const int e = ids[static_cast<long long>(t) * k + j] - e_lo;
+    const uint16_t* wr = w_down + (static_cast<long long>(e) * H + col) * I + k0;
+    const uint16_t* hr = h + static_cast<long long>(p) * I + k0;
+    const uint16_t* lr = h_lo ? h_lo + static_cast<long long>(p) * I + k0 : nullptr;
+    // 8 partial sums, one per bf16 position of a 16-byte vector, so consecutive vectors' loads
+    // and FMAs are independent and several loads stay in flight
+    float d[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int kk = 0; kk < per; kk += 8) {
+      const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(wr + kk);
+      const u32x4_t hv = *reinterpret_cast<const u32x4_t*>(hr + kk);
+      u32x4_t lv = {0u, 0u, 0u, 0u};
+      if (lr) lv = *reinterpret_cast<const u32x4_t*>(lr + kk);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float h0 = __uint_as_float(hv[i] << 16) + __uint_as_float(lv[i] << 16);
+        const float h1 = __uint_as_float(hv[i] & 0xffff0000u) + __uint_as_float(lv[i] & 0xffff0000u);
+        d[2 * i] = fmaf(h0, __uint_as_float(wv[i] << 16), d[2 * i]);
+        d[2 * i + 1] = fmaf(h1, __uint_as_float(wv[i] & 0xffff0000u), d[2 * i + 1]);
+      }
+    }
+    part[q][c] = ((d[0] + d[1]) + (d[2] + d[3])) + ((d[4] + d[5]) + (d[6] + d[7]));
+    __syncthreads();
+    if (q == 0) {
+      float y = 0.f;
+#pragma unroll
+      for (int s = 0; s < kDcSlices; ++s) y += part[s][c];
+      acc += wts[static_cast<long long>(t) * k + j] * y;
+    }
+    __syncthreads();
+  }
+  if (q != 0) return;
+  if (shared_y) {
+    for (int s = 0; s < shared_n; ++s) {
+      const long long off = (static_cast<long long>(s) * T + t) * H + col;
+      acc += shared_dtype == kBF16 ? bf16_to_f32(static_cast<const uint16_t*>(shared_y)[off])
+                                   : static_cast<const float*>(shared_y)[off];
+    }
+  }
+  const long long o = static_cast<long long>(t) * H + col;
+  if (out_dtype == kBF16) static_cast<uint16_t*>(out)[o] = f32_to_bf16(acc);
+  else static_cast<float*>(out)[o] = acc;
+}
+
+bool down_combine_supported(int H, int I) { return H % kDcCols == 0 && I % (8 * kDcSlices) == 0; }
+
+hipError_t launch_down_combine(const void* h, const void* h_lo, const void* w_down, int I, int H, const int32_t* ids,
+                               const float* w, const int32_t* pos, int T, int k, int e_lo, const void* shared_y,
+                               int shared_dtype, int shared_n, void* out, int out_dtype, hipStream_t s) {
+  if (!down_combine_supported(H, I) || T < 1 || T > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(down_combine_kernel, dim3(H / kDcCols, T), dim3(kDcCols * kDcSlices), 0, s,
+                     static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(h_lo),
+                     static_cast<const uint16_t*>(w_down), I, H, ids, w, pos, k, e_lo, shared_y, shared_dtype,
+                     shared_n, T, out, out_dtype);
+  return hipGetLastError();
+}
+
 }  // namespace eimoe

@@ -200,7 +200,7 @@ def test_layer_real_shape(dev, name, T):
 
 
 @pytest.mark.parametrize("name", ["mixtral-8x7b", "deepseek-v2-lite", "qwen3-30b-a3b-local32"])
-@pytest.mark.parametrize("T", [3, 200])
+@pytest.mark.parametrize("T", [1, 3, 200])
 def test_layer_precise_mode_tracks_fp32(dev, name, T):
     """h_split keeps ~16 significant bits of h, so the layer tracks the fp32 oracle ~100x closer
     than the default bf16 intermediate (both routed and shared experts go through it)."""
