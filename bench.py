@@ -51,7 +51,8 @@ def parse():
     ap.add_argument("--no-suite", action="store_true",
                     help="skip the other workloads (tiny fp32 layer, DeepSeek-V2-Lite, Qwen3-30B-A3B local share, "
                          "fp8 Mixtral)")
-    ap.add_argument("--profile-case", default=None, metavar="NAME:T[:uniform][:w8a8] | prologue:T:H:E[:f32]",
+    ap.add_argument("--profile-case", default=None,
+                    metavar="NAME:T[:uniform][:w8a8] | prologue:T:H:E[:f32] | copy",
                     help="profiling driver: 12 cache-flushed fused-layer calls of one workload (names as in "
                          "easyinfra_amd.workloads.SHAPES); prints no JSON line")
     ap.add_argument("--traffic-run", action="store_true",
@@ -329,6 +330,14 @@ def suite(torch, ops, mix_inp, steps, warmup):
 def profile_case(torch, ops, spec):
     from easyinfra_amd.workloads import SHAPES, make_inputs
     parts = spec.split(":")
+    if parts[0] == "copy":   # counter calibration: a 1 GiB device copy (1 GiB read + 1 GiB written)
+        src = torch.empty(512 << 20, dtype=torch.bfloat16, device="cuda").normal_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print("profile case done:", spec, flush=True)
+        return
     if parts[0] == "prologue":   # prologue:T:H:E[:f32] -- residual add + RMSNorm + router logits
         T, H, E = (int(v) for v in parts[1:4])
         g = torch.Generator(device="cuda").manual_seed(T + E)
