@@ -61,6 +61,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, lo
                                            kBufDword3);
 }
 
+// A wave-uniform value, taken from the first lane.  Buffer windows and tile coordinates are
+// uniform by construction, but where they derive from values read out of LDS (the tile
+// decode) the compiler cannot prove it: it then keeps them in VGPRs and wraps every buffer
+// instruction in a readfirstlane loop (measured: 8 such loops per K slab in the 256x256
+// e4m3 kernel).  Taking them from the first lane once, at the tile's start, keeps them in SGPRs.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ long long uniform(long long v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  return static_cast<long long>(
+      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32))) << 32) |
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u)));
+}
+template <class T>
+__device__ __forceinline__ T* uniform(T* p) {
+  return reinterpret_cast<T*>(uniform(reinterpret_cast<long long>(p)));
+}
+
 // Wave-wide inclusive prefix sum (64 lanes).
 __device__ __forceinline__ int wave_incl_scan(int v) {
   const int lane = threadIdx.x & 63;

@@ -149,10 +149,11 @@ __device__ __forceinline__ bool decode_tile(const GemmArgs& p, int* s_pref, Tile
   const int m_tile = grp * GM + (r_in - tc.n_tile * gm);
   const int seg_r0 = min(max(p.seg_off[seg], 0), p.max_rows);
   const int seg_r1 = min(max(p.seg_off[seg + 1], seg_r0), p.max_rows);
-  tc.row0 = seg_r0 + m_tile * BM;
-  tc.row_end = min(tc.row0 + BM, seg_r1);
-  tc.expert = seg % p.e_mod;
-  tc.split = split;
+  tc.row0 = uniform(seg_r0 + m_tile * BM);
+  tc.row_end = uniform(min(seg_r0 + m_tile * BM + BM, seg_r1));
+  tc.expert = uniform(seg % p.e_mod);
+  tc.split = uniform(split);
+  tc.n_tile = uniform(tc.n_tile);
   return true;
 }
 
@@ -259,30 +260,42 @@ __device__ __forceinline__ void slab_mma(f32x4_t (&acc)[MBE][G::NB], const uint1
 }
 
 // Epilogue: lane owns rows 4*(lane/16)+r of each 16-row fragment and NI adjacent columns.
+// The fp8 scales are all loaded before the first store: loaded between stores (which may
+// alias them, as far as the compiler knows) each row's loads would wait for the previous
+// row's, a chain of 16 memory latencies that measured ~12 us per 256x256 e4m3 tile.
 template <class G, int EPI, int MBE>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc, f32x4_t (&acc)[MBE][G::NB], int wm,
                                          int wn, int lane, const float* scale) {
   const int lr = lane & 15;
   const int lq = lane >> 4;
+  const int col0 = G::SILU ? tc.n_tile * G::OUT_BN + wn * (G::WN / 2) + lr * G::NI
+                           : tc.n_tile * G::OUT_BN + wn * G::WN + lr * G::NI;
+  float cs[G::NI], cs_up[G::SILU ? G::NI : 1];   // per-output-channel weight scales
+#pragma unroll
+  for (int j = 0; j < G::NI; ++j) {
+    cs[j] = scale ? scale[col0 + j] : 1.f;
+    if constexpr (G::SILU) cs_up[j] = scale ? scale[p.up_off + col0 + j] : 1.f;
+  }
+  float rs[MBE][4];   // fp8 activations: per-row scale of the A row each output row came from
+#pragma unroll
+  for (int i = 0; i < MBE; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = tc.row0 + wm * 16 * MBE + i * 16 + lq * 4 + r;
+      rs[i][r] = p.a_scale && row < tc.row_end ? p.a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
+    }
 #pragma unroll
   for (int i = 0; i < MBE; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = tc.row0 + wm * 16 * MBE + i * 16 + lq * 4 + r;
       if (row >= tc.row_end) continue;
-      // fp8 activations: per-row scale of the A row this output row came from
-      const float rs = p.a_scale ? p.a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
       if constexpr (G::SILU) {
-        const int col0 = tc.n_tile * G::OUT_BN + wn * (G::WN / 2) + lr * G::NI;
         float h[G::NI];
 #pragma unroll
         for (int j = 0; j < G::NI; ++j) {
-          float g = acc[i][j][r] * rs;
-          float u = acc[i][j + G::NI][r] * rs;
-          if (scale) {
-            g *= scale[col0 + j];
-            u *= scale[p.up_off + col0 + j];
-          }
+          const float g = acc[i][j][r] * rs[i][r] * cs[j];
+          const float u = acc[i][j + G::NI][r] * rs[i][r] * cs_up[j];
           h[j] = silu_f32(g) * u;
         }
         const long long off = static_cast<long long>(row) * p.ldc + col0;
@@ -297,10 +310,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
           store_bf16<G::NI>(static_cast<uint16_t*>(p.c_lo) + off, h);
         }
       } else {
-        const int col0 = tc.n_tile * G::OUT_BN + wn * G::WN + lr * G::NI;
         float v[G::NI];
 #pragma unroll
-        for (int j = 0; j < G::NI; ++j) v[j] = acc[i][j][r] * rs * (scale ? scale[col0 + j] : 1.f);
+        for (int j = 0; j < G::NI; ++j) v[j] = acc[i][j][r] * rs[i][r] * cs[j];
         const long long off =
             static_cast<long long>(tc.split) * p.c_split_stride + static_cast<long long>(row) * p.ldc + col0;
         if constexpr (EPI == kEpiStoreF32) store_f32<G::NI>(static_cast<float*>(p.c) + off, v);
@@ -506,6 +518,46 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
   });
 }
 
+// ---------------------------------------------------------------------------- e4m3 fragments (W8A8)
+// Both operands OCP e4m3fn on v_mfma_scale_f32_16x16x128_f8f6f4 (block scales fixed at
+// 1.0; the per-row activation scale and per-output-channel weight scale are applied in
+// the epilogue).  A 128-wide fp8 K slab is one 128-byte LDS row, so slab loading,
+// swizzle and staging are those of the bf16 kernels.  Each lane feeds 32 bytes per
+// operand: 16-byte chunks q and q+4 of its row (lane group q = lane/16); A and B use the
+// same K assignment, so the K sum is exact whatever order the instruction adds.
+__device__ __forceinline__ i32x8_t frag_fp8(const uint8_t* s, int R, int q) {
+  const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(&s[R * 128 + ((q ^ swz(R)) << 4)]);
+  const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(&s[R * 128 + (((q + 4) ^ swz(R)) << 4)]);
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+__device__ __forceinline__ f32x4_t mfma_fp8(const i32x8_t& a, const i32x8_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// One 128-wide slab in two halves of the B fragments: the A fragments and half of the B
+// fragments are live at once (64 VGPRs for the 256x256 tile, not 96).
+template <class G, int MBE>
+__device__ __forceinline__ void slab_mma_fp8(f32x4_t (&acc)[MBE][G::NB], const uint8_t* sA, const uint8_t* sB,
+                                             int wm, int wn, int lane) {
+  constexpr int NH = G::NB % 2 == 0 ? G::NB / 2 : G::NB;
+  const int lr = lane & 15;
+  const int q = lane >> 4;
+  i32x8_t af[MBE];
+#pragma unroll
+  for (int i = 0; i < MBE; ++i) af[i] = frag_fp8(sA, wm * 16 * MBE + i * 16 + lr, q);
+#pragma unroll
+  for (int h = 0; h < G::NB; h += NH) {
+    i32x8_t bfr[NH];
+#pragma unroll
+    for (int j = 0; j < NH; ++j) bfr[j] = frag_fp8(sB, wn * G::WN + (h + j) * 16 + lr, q);
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int j = 0; j < NH; ++j) acc[i][h + j] = mfma_fp8(af[i], bfr[j], acc[i][h + j]);
+  }
+}
+
 // ---------------------------------------------------------------------------- bf16 ping-pong
 // The 256x256 tile with its 8 waves in two groups of four, one wave of each group per SIMD
 // (waves w and w + 4).  The groups run one phase apart: while one group multiplies the slab
@@ -530,7 +582,7 @@ __device__ __forceinline__ void pp_barrier() {
 __device__ __forceinline__ void pp_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }     // vmcnt(0)
 __device__ __forceinline__ void pp_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }   // lgkmcnt(0)
 
-// ---------------------------------------------------------------------------- bf16 ping-pong, three B stages
+// ---------------------------------------------------------------------------- ping-pong, three B stages (bf16 or e4m3)
 // The ping-pong kernel with the weight panel (B, the operand streamed from HBM) fetched two slabs
 // ahead: A in two stages, B in three, 5 x 32 KiB = the whole 160 KiB of LDS (the segment prefix
 // lives in the third B stage until that stage's first load).  At the top of slab kt every wave
@@ -557,14 +609,74 @@ __device__ __forceinline__ void issue_ab_dma(const BufRef& a, const BufRef& b, c
 #endif
 }
 
-template <int EPI, int GM>
+// Phases of the ping-pong loop.  bf16: phase KK reads the A and B fragments of K half KK (32
+// wide) and runs MBE x NB MFMAs.  e4m3 (one 16x16x128 MFMA covers a 128-byte row): phase 0
+// reads the A fragments and the first half of the B fragments, phase 1 the other half of B,
+// and each runs MBE x NB/2 MFMAs of twice the bf16 MFMA's cycles, so a phase is the same MFMA
+// time either way and the live fragments stay at 64 VGPRs.
+template <bool FP8, class G, int MBE>
+struct PpFrags;
+template <class G, int MBE>
+struct PpFrags<false, G, MBE> {
+  bf16x8_t a[MBE], b[G::NB];
+};
+template <class G, int MBE>
+struct PpFrags<true, G, MBE> {
+  i32x8_t a[MBE], b[G::NB / 2];
+};
+
+template <bool FP8, class G, int MBE, int KK>
+__device__ __forceinline__ void pp_read(PpFrags<FP8, G, MBE>& f, const uint16_t* sA, const uint16_t* sB, int wm,
+                                        int wn, int lane) {
+  if constexpr (!FP8) {
+    read_frags<G, MBE>(sA, sB, KK, wm, wn, lane, f.a, f.b);
+  } else {
+    const int lr = lane & 15;
+    const int q = lane >> 4;
+    if constexpr (KK == 0) {
+#pragma unroll
+      for (int i = 0; i < MBE; ++i) f.a[i] = frag_fp8(reinterpret_cast<const uint8_t*>(sA), wm * 16 * MBE + i * 16 + lr, q);
+    }
+#pragma unroll
+    for (int j = 0; j < G::NB / 2; ++j)
+      f.b[j] = frag_fp8(reinterpret_cast<const uint8_t*>(sB), wn * G::WN + (KK * G::NB / 2 + j) * 16 + lr, q);
+  }
+}
+
+template <bool FP8, class G, int MBE, int KK>
+__device__ __forceinline__ void pp_mma(f32x4_t (&acc)[MBE][G::NB], const PpFrags<FP8, G, MBE>& f) {
+  if constexpr (!FP8) {
+    mma<G, MBE>(acc, f.a, f.b);
+  } else {
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int j = 0; j < G::NB / 2; ++j)
+        acc[i][KK * G::NB / 2 + j] = mfma_fp8(f.a[i], f.b[j], acc[i][KK * G::NB / 2 + j]);
+    // Phase 0's accumulators are not read again until the next slab, and the machine sinking
+    // pass would move their MFMAs past the phase barrier into phase 1 (measured: all 32 MFMAs
+    // of a slab then run in one phase).  An empty asm that takes them as operands keeps them here.
+    if constexpr (KK == 0) {
+#pragma unroll
+      for (int i = 0; i < MBE; ++i)
+#pragma unroll
+        for (int j = 0; j < G::NB / 2; ++j) asm volatile("" ::"v"(acc[i][j]));
+    }
+  }
+}
+
+// FP8: e4m3 activations and weights (W8A8); an LDS row is 128 bytes either way (64 bf16 or 128
+// e4m3 of K per slab), so the DMA, the swizzle and the stages are the same bytes.
+template <int EPI, int GM, bool FP8 = false>
 __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
   using G = Geo<256, 256, 4, 2, EPI>;
   constexpr int BK = G::BK;
+  constexpr int EB = FP8 ? 1 : 2;             // bytes per element
   constexpr int NW = G::NW;
   constexpr int A_PW = 256 / 8 / G::NW;
   constexpr int B_PW = 256 / 8 / G::NW;
   static_assert(B_PW == 4, "the slab-end wait is vmcnt(B_PW)");
+  static_assert(!FP8 || G::NB % 2 == 0, "e4m3 phases split the B fragments in two");
   static_assert((kMaxSeg + 1) * sizeof(int) <= 256 * BK * sizeof(uint16_t), "segment prefix fits a B stage");
   __shared__ __attribute__((aligned(1024))) uint16_t sA0[256 * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sA1[256 * BK];
@@ -581,22 +693,22 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
   const int lrow = lane >> 3;
   const long long k0 = static_cast<long long>(tc.split) * p.K;
 
-  const BufRef rA{static_cast<const uint16_t*>(p.a) + k0, (p.a_rows_cap * p.lda - k0) * 2};
+  const BufRef rA{static_cast<const uint8_t*>(p.a) + k0 * EB, (p.a_rows_cap * p.lda - k0) * EB};
   uint32_t a_voff[A_PW];
-  a_offsets<A_PW, NW>(p, tc, wave, lane, 2, a_voff);
-  const uint16_t* b_base = reinterpret_cast<const uint16_t*>(expert_weights(p, tc.expert, 2)) + k0;
-  const BufRef rB{b_base, (p.b_estride - k0) * 2};
+  a_offsets<A_PW, NW>(p, tc, wave, lane, EB, a_voff);
+  const BufRef rB{expert_weights(p, tc.expert, EB) + k0 * EB, (p.b_estride - k0) * EB};
   uint32_t b_voff[B_PW];
 #pragma unroll
   for (int i = 0; i < B_PW; ++i) {
     const int R = (wave * B_PW + i) * 8 + lrow;
     const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
-    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb * 2 + (((lane & 7) ^ swz(R)) << 4));
+    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb * EB + (((lane & 7) ^ swz(R)) << 4));
   }
+  const float* scale = FP8 ? p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows : nullptr;
 
   const int wm = wave % 4;
   const int wn = wave / 4;
-  const int KT = p.K / BK;
+  const int KT = p.K * EB / (BK * 2);        // 128-byte slabs
   by_height<256, G::MB, A_PW>(tc.row_end - tc.row0, [&]<int MBE>() {
     constexpr int A_CNT = A_PW * MBE / G::MB;
     f32x4_t acc[MBE][G::NB];
@@ -612,14 +724,14 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
     pp_wait_vm0();
     pp_barrier();
     if (grp == 1) pp_barrier();
-    bf16x8_t af[MBE], bfr[G::NB];
-#define EIMOE_PP3_HALF(SA, SB, KK)                         \
-    read_frags<G, MBE>(SA, SB, KK, wm, wn, lane, af, bfr); \
-    pp_wait_lgkm0();                                       \
-    if (KK == 1 && grp == 1) pp_wait_vm4();                \
-    pp_barrier();                                          \
-    mma<G, MBE>(acc, af, bfr);                             \
-    if (KK == 1 && grp == 0) pp_wait_vm4();                \
+    PpFrags<FP8, G, MBE> fr;
+#define EIMOE_PP3_HALF(SA, SB, KK)                        \
+    pp_read<FP8, G, MBE, KK>(fr, SA, SB, wm, wn, lane);   \
+    pp_wait_lgkm0();                                      \
+    if (KK == 1 && grp == 1) pp_wait_vm4();               \
+    pp_barrier();                                         \
+    pp_mma<FP8, G, MBE, KK>(acc, fr);                     \
+    if (KK == 1 && grp == 0) pp_wait_vm4();               \
     pp_barrier();
     // slab kt + J: read (SA, SB); load A(kt+J+1) into SAN and B(kt+J+2) into SBN (clamped to
     // the last slab near the end: those stages are not read again)
@@ -642,48 +754,8 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
 #undef EIMOE_PP3_HALF
     if (grp == 0) pp_barrier();   // matches group 1's late start
     pp_wait_vm0();                // the clamped loads near the end land before the LDS is released
-    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr);
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale);
   });
-}
-
-// ---------------------------------------------------------------------------- fp8 x fp8 (W8A8)
-// Both operands OCP e4m3fn on v_mfma_scale_f32_16x16x128_f8f6f4 (block scales fixed at
-// 1.0; the per-row activation scale and per-output-channel weight scale are applied in
-// the epilogue).  A 128-wide fp8 K slab is one 128-byte LDS row, so slab loading,
-// swizzle and double buffering are those of the bf16 kernel.  Each lane feeds 32 bytes
-// per operand: 16-byte chunks q and q+4 of its row (lane group q = lane/16); A and B
-// use the same K assignment, so the K sum is exact whatever order the instruction adds.
-template <class G, int MBE>
-__device__ __forceinline__ void read_frags_fp8(const uint8_t* sA, const uint8_t* sB, int wm, int wn, int lane,
-                                               i32x8_t (&af)[MBE], i32x8_t (&bfr)[G::NB]) {
-  const int lr = lane & 15;
-  const int q = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < MBE; ++i) {
-    const int R = wm * 16 * MBE + i * 16 + lr;
-    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(&sA[R * 128 + ((q ^ swz(R)) << 4)]);
-    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(&sA[R * 128 + (((q + 4) ^ swz(R)) << 4)]);
-    af[i] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-  }
-#pragma unroll
-  for (int j = 0; j < G::NB; ++j) {
-    const int R = wn * G::WN + j * 16 + lr;
-    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(&sB[R * 128 + ((q ^ swz(R)) << 4)]);
-    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(&sB[R * 128 + (((q + 4) ^ swz(R)) << 4)]);
-    bfr[j] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-  }
-}
-
-template <class G, int MBE>
-__device__ __forceinline__ void slab_mma_fp8(f32x4_t (&acc)[MBE][G::NB], const uint8_t* sA, const uint8_t* sB,
-                                             int wm, int wn, int lane) {
-  i32x8_t af[MBE], bfr[G::NB];
-  read_frags_fp8<G, MBE>(sA, sB, wm, wn, lane, af, bfr);
-#pragma unroll
-  for (int i = 0; i < MBE; ++i)
-#pragma unroll
-    for (int j = 0; j < G::NB; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bfr[j], acc[i][j], 0, 0, 0, 127, 0, 127);
 }
 
 template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
@@ -854,12 +926,15 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
   return hipGetLastError();
 }
 
-// bf16 256x256 tiles: the ping-pong kernel (3-4 % faster than the lock-step 8-wave kernel on
-// the Mixtral-8x7B prefill GEMMs, bit-identical results).
+// 256x256 tiles: the ping-pong kernel (bf16: 3-4 % faster than the lock-step 8-wave kernel on
+// the Mixtral-8x7B prefill GEMMs, bit-identical results; e4m3 W8A8: with the epilogue's scale
+// loads hoisted, gate/up 2.32 -> 1.95 ms and down (K split 2) 1.08 -> 0.89 ms against the
+// lock-step kernel, A/B on one box).  W8A16 keeps the lock-step kernel (its B goes through
+// registers for the conversion).
 // Tile grouping depth 4.  16 measured 3 % faster on the bare Mixtral prefill GEMMs (gate/up
 // 3.16 vs 3.25 ms) but not on whole layers (Mixtral 8192 tokens 4.94-4.98 vs 4.92-4.95 ms;
 // DeepSeek-V2-Lite and Qwen3 within noise), so the layer's figure decides.
-template <int EPI, int GMX = 4>
+template <int EPI, bool FP8 = false, int GMX = 4>
 static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
   constexpr int OUT_BN = epi_silu(EPI) ? 128 : 256;
   const int n_tiles = p.N / OUT_BN;
@@ -868,7 +943,8 @@ static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
   long long grid = (total + kNumXcd - 1) / kNumXcd * kNumXcd;
   if (grid < kNumXcd) grid = kNumXcd;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((grouped_gemm_pp3_kernel<EPI, GMX>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, s, p);
+  hipLaunchKernelGGL((grouped_gemm_pp3_kernel<EPI, GMX, FP8>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, s,
+                     p);
   return hipGetLastError();
 }
 
@@ -876,8 +952,12 @@ template <int EPI, bool BFP8>
 static hipError_t launch_epi(const GemmArgs& p, int max_rows, int tile, bool a_fp8, hipStream_t s) {
   switch (tile) {
     case kTileL:
-      if constexpr (BFP8) return launch_cfg<256, 256, 4, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
-      else return launch_pp<EPI>(p, max_rows, s);
+      if constexpr (BFP8) {
+        if (a_fp8) return launch_pp<EPI, true>(p, max_rows, s);
+        return launch_cfg<256, 256, 4, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
+      } else {
+        return launch_pp<EPI>(p, max_rows, s);
+      }
     case kTileM: return launch_cfg<128, 128, 2, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
     case kTileS: return launch_cfg<32, 128, 1, 4, EPI, BFP8, 1>(p, max_rows, a_fp8, s);
     case kTileXS: return launch_cfg<16, 64, 1, 2, EPI, BFP8, 1>(p, max_rows, a_fp8, s);
