@@ -69,9 +69,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, lo
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ long long uniform(long long v) {
   const uint64_t u = static_cast<uint64_t>(v);
-  return static_cast<long long>(
-      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32))) << 32) |
-      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u)));
+  // each half as uint32_t: the builtin returns int, and a sign-extended low half would set
+  // every bit of the high half (a pointer with address bit 31 set would become 0xffffffff...)
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32)));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u)));
+  return static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 template <class T>
 __device__ __forceinline__ T* uniform(T* p) {
