@@ -585,10 +585,13 @@ __device__ __forceinline__ void pp_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC
 // ---------------------------------------------------------------------------- ping-pong, three B stages (bf16 or e4m3)
 // The ping-pong kernel with the weight panel (B, the operand streamed from HBM) fetched two slabs
 // ahead: A in two stages, B in three, 5 x 32 KiB = the whole 160 KiB of LDS (the segment prefix
-// lives in the third B stage until that stage's first load).  At the top of slab kt every wave
-// issues A(kt+1) then B(kt+2); the slab ends waiting for all but the last B_PW loads of the wave
-// (vmcnt(4): loads complete in issue order), so A(kt+1) and B(kt+1) have landed and B(kt+2) may
-// still be in flight.  Unrolled by six so every stage index is static.
+// lives in the third B stage until that stage's first load).  Each wave issues A(kt+1) at the top
+// of its first phase of slab kt and B(kt+2) at the top of its second: issuing both in one phase
+// made that phase longer than the other group's multiply (the ping-pong's MFMA-idle gap; moving B
+// to the second phase took the Mixtral-8x7B prefill layer from 4.84 to 4.43 ms, A/B on one box).
+// The slab ends waiting for all but the last B_PW loads of the wave (vmcnt(4): loads complete in
+// issue order), so A(kt+1) and B(kt+1) have landed and B(kt+2) may still be in flight.  Unrolled by
+// six so every stage index is static.
 __device__ __forceinline__ void pp_wait_vm4() { __builtin_amdgcn_s_waitcnt(0x0F74); }   // vmcnt(4)
 
 template <int A_CNT, int B_PW, int NW, int A_PW>
@@ -737,9 +740,9 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
     // the last slab near the end: those stages are not read again)
 #define EIMOE_PP3_SLAB(J, SA, SB, SAN, SBN)                                                              \
     if (kt + J < KT) {                                                                                   \
-      issue_ab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, min(kt + J + 1, KT - 1) * BK * 2, \
-                                    min(kt + J + 2, KT - 1) * BK * 2);                                   \
+      issue_a_dma<A_CNT, NW>(rA, a_voff, SAN, wave, min(kt + J + 1, KT - 1) * BK * 2);                   \
       EIMOE_PP3_HALF(SA, SB, 0)                                                                          \
+      issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, 0, min(kt + J + 2, KT - 1) * BK * 2); \
       EIMOE_PP3_HALF(SA, SB, 1)                                                                          \
     }
     for (int kt = 0; kt < KT; kt += 6) {
