@@ -728,8 +728,16 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
     pp_barrier();
     if (grp == 1) pp_barrier();
     PpFrags<FP8, G, MBE> fr;
-#define EIMOE_PP3_HALF(SA, SB, KK)                        \
+    // The phase's DMA goes ahead of its fragment reads for bf16, after them for e4m3 (A/B on one
+    // box: bf16 prefill 4.47 vs 4.50 ms; W8A8 prefill 2.76 vs 2.65 ms).
+#define EIMOE_PP3_HALF(SA, SB, KK, DMA)                   \
+    if constexpr (!FP8) DMA;                              \
     pp_read<FP8, G, MBE, KK>(fr, SA, SB, wm, wn, lane);   \
+    if constexpr (FP8) {                                  \
+      pin_issue();                                        \
+      DMA;                                                \
+      pin_issue();                                        \
+    }                                                     \
     pp_wait_lgkm0();                                      \
     if (KK == 1 && grp == 1) pp_wait_vm4();               \
     pp_barrier();                                         \
@@ -740,10 +748,10 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
     // the last slab near the end: those stages are not read again)
 #define EIMOE_PP3_SLAB(J, SA, SB, SAN, SBN)                                                              \
     if (kt + J < KT) {                                                                                   \
-      issue_a_dma<A_CNT, NW>(rA, a_voff, SAN, wave, min(kt + J + 1, KT - 1) * BK * 2);                   \
-      EIMOE_PP3_HALF(SA, SB, 0)                                                                          \
-      issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, 0, min(kt + J + 2, KT - 1) * BK * 2); \
-      EIMOE_PP3_HALF(SA, SB, 1)                                                                          \
+      EIMOE_PP3_HALF(SA, SB, 0, (issue_a_dma<A_CNT, NW>(rA, a_voff, SAN, wave, min(kt + J + 1, KT - 1) * BK * 2))) \
+      EIMOE_PP3_HALF(SA, SB, 1,                                                                          \
+                     (issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, 0,                \
+                                                min(kt + J + 2, KT - 1) * BK * 2)))                      \
     }
     for (int kt = 0; kt < KT; kt += 6) {
       EIMOE_PP3_SLAB(0, sA0, sB0, sA1, sB2)
