@@ -256,23 +256,34 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   }
 
   const int lq = lane >> 4;
+  // The e4m3 scales are loaded before the first store: loads between stores that may alias
+  // them would wait for each other, a chain of memory latencies per row.
+  // bf16 operands carry no scales (the products fold away at compile time); e4m3 operands always
+  // carry both (the W8A8 entry points require them).
+  float cs[NFRAG];   // per-output-channel weight scales of this lane's fragment columns
+  float rsv[MBLK][4];   // per-row activation scales
+#pragma unroll
+  for (int f = 0; f < NFRAG; ++f)
+    cs[f] = FP8 ? p.b_scale[static_cast<long long>(expert) * p.nb_rows + wrow[f]] : 1.f;
+#pragma unroll
+  for (int m = 0; m < MBLK; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + m * 16 + lq * 4 + r;
+      rsv[m][r] = FP8 && row < row_end ? p.a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
+    }
 #pragma unroll
   for (int m = 0; m < MBLK; ++m) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = row0 + m * 16 + lq * 4 + r;
       if (row >= row_end) continue;
-      const float rs = p.a_scale ? p.a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
+      const float rs = rsv[m][r];
       if constexpr (SILU) {
 #pragma unroll
         for (int f = 0; f < G; ++f) {
-          float g = acc[m][f][r] * rs;
-          float u = acc[m][G + f][r] * rs;
-          if (p.b_scale) {
-            const float* sc = p.b_scale + static_cast<long long>(expert) * p.nb_rows;
-            g *= sc[wrow[f]];
-            u *= sc[wrow[G + f]];
-          }
+          const float g = acc[m][f][r] * rs * cs[f];
+          const float u = acc[m][G + f][r] * rs * cs[G + f];
           const float h = silu_f32(g) * u;
           const uint16_t hb = f32_to_bf16(h);
           const long long off = static_cast<long long>(row) * p.ldc + col0 + f * 16 + lr;
@@ -285,8 +296,7 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
           const int col = col0 + f * 16 + lr;
           const long long off =
               static_cast<long long>(split) * p.c_split_stride + static_cast<long long>(row) * p.ldc + col;
-          const float v =
-              acc[m][f][r] * rs * (p.b_scale ? p.b_scale[static_cast<long long>(expert) * p.nb_rows + wrow[f]] : 1.f);
+          const float v = acc[m][f][r] * rs * cs[f];
           if constexpr (EPI == kEpiStoreF32) static_cast<float*>(p.c)[off] = v;
           else static_cast<uint16_t*>(p.c)[off] = f32_to_bf16(v);
         }
