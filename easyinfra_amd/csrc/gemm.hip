@@ -263,9 +263,11 @@ __device__ __forceinline__ void slab_mma(f32x4_t (&acc)[MBE][G::NB], const uint1
 // The fp8 scales are all loaded before the first store: loaded between stores (which may
 // alias them, as far as the compiler knows) each row's loads would wait for the previous
 // row's, a chain of 16 memory latencies that measured ~12 us per 256x256 e4m3 tile.
+// scale: per-output-channel weight scales, a_scale: per-row activation scales (either may be
+// null; the bf16 kernels pass compile-time nulls, so their epilogue has no scale arithmetic).
 template <class G, int EPI, int MBE>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc, f32x4_t (&acc)[MBE][G::NB], int wm,
-                                         int wn, int lane, const float* scale) {
+                                         int wn, int lane, const float* scale, const float* a_scale) {
   const int lr = lane & 15;
   const int lq = lane >> 4;
   const int col0 = G::SILU ? tc.n_tile * G::OUT_BN + wn * (G::WN / 2) + lr * G::NI
@@ -282,7 +284,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = tc.row0 + wm * 16 * MBE + i * 16 + lq * 4 + r;
-      rs[i][r] = p.a_scale && row < tc.row_end ? p.a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
+      rs[i][r] = a_scale && row < tc.row_end ? a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
     }
 #pragma unroll
   for (int i = 0; i < MBE; ++i) {
@@ -514,7 +516,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
       __syncthreads();
     }
     if (kt < KT) slab_mma<G, MBE, F32>(acc, sA0, sB0, wm, wn, lane);   // odd slab count: last slab in buffer 0
-    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr);
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr, nullptr);
   });
 }
 
@@ -765,7 +767,7 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
 #undef EIMOE_PP3_HALF
     if (grp == 0) pp_barrier();   // matches group 1's late start
     pp_wait_vm0();                // the clamped loads near the end land before the LDS is released
-    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale);
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale, FP8 ? p.a_scale : nullptr);
   });
 }
 
@@ -835,7 +837,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8_kernel(GemmAr
       __syncthreads();
     }
     if (kt < KT) slab_mma_fp8<G, MBE>(acc, sA0, sB0, wm, wn, lane);
-    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale);
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale, p.a_scale);
   });
 }
 
@@ -910,7 +912,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8w_kernel(GemmA
       if (kt + 1 < KT) store_b_fp8<G, B_LD, B_CH, NT>(rb, b_R, b_c, sB[cur ^ 1]);
       __syncthreads();
     }
-    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale);
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale, nullptr);   // W8A16: bf16 activations
   });
 }
 
