@@ -260,32 +260,85 @@ __device__ __forceinline__ void slab_mma(f32x4_t (&acc)[MBE][G::NB], const uint1
 }
 
 // Epilogue: lane owns rows 4*(lane/16)+r of each 16-row fragment and NI adjacent columns.
-// The fp8 scales are all loaded before the first store: loaded between stores (which may
-// alias them, as far as the compiler knows) each row's loads would wait for the previous
-// row's, a chain of 16 memory latencies that measured ~12 us per 256x256 e4m3 tile.
-// scale: per-output-channel weight scales, a_scale: per-row activation scales (either may be
-// null; the bf16 kernels pass compile-time nulls, so their epilogue has no scale arithmetic).
-template <class G, int EPI, int MBE>
-__device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc, f32x4_t (&acc)[MBE][G::NB], int wm,
-                                         int wn, int lane, const float* scale, const float* a_scale) {
-  const int lr = lane & 15;
-  const int lq = lane >> 4;
-  const int col0 = G::SILU ? tc.n_tile * G::OUT_BN + wn * (G::WN / 2) + lr * G::NI
-                           : tc.n_tile * G::OUT_BN + wn * G::WN + lr * G::NI;
-  float cs[G::NI], cs_up[G::SILU ? G::NI : 1];   // per-output-channel weight scales
+// Scales: per-output-channel weight scales (scale) and per-row activation scales (a_scale);
+// either may be null, and the bf16 kernels pass compile-time nulls, so their epilogue has no
+// scale arithmetic.  All are loaded before the first store: loaded between stores (which may
+// alias them, as far as the compiler knows) each row's loads would wait for the previous row's,
+// a chain of 16 memory latencies that measured ~12 us per 256x256 e4m3 tile.
+template <class G, int MBE>
+struct EpiScales {
+  float cs[G::NI], cs_up[G::SILU ? G::NI : 1];   // weight scales of the lane's output columns
+  float rs[MBE][4];                              // activation scale of each of the lane's rows
+};
+
+template <class G, int MBE>
+__device__ __forceinline__ int epi_col0(const TileCoord& tc, int wn, int lane) {
+  return G::SILU ? tc.n_tile * G::OUT_BN + wn * (G::WN / 2) + (lane & 15) * G::NI
+                 : tc.n_tile * G::OUT_BN + wn * G::WN + (lane & 15) * G::NI;
+}
+
+// Two steps, so that a caller can put other loads between them: the weight scales and the
+// row map (rows past the segment take the last row, whose scale is never stored: no per-row
+// branch, so the row-map loads issue back to back; with a branch per row the compiler waited for
+// each row's dependent pair in turn, 16 round trips, ~3.5 us per 256x256 tile), then the
+// activation scales of the mapped rows.
+// The null tests sit outside the loops: tested per element, they split the loads into one
+// block each, and the wait inserted at every block waited for the loads in flight before it.
+template <class G, int MBE>
+__device__ __forceinline__ void epi_load_scales_1(const GemmArgs& p, const TileCoord& tc, int wm, int wn, int lane,
+                                                  const float* scale, const float* a_scale, EpiScales<G, MBE>& sc,
+                                                  int (&src_row)[MBE][4]) {
+  const int col0 = epi_col0<G, MBE>(tc, wn, lane);
+  if (scale) {
 #pragma unroll
-  for (int j = 0; j < G::NI; ++j) {
-    cs[j] = scale ? scale[col0 + j] : 1.f;
-    if constexpr (G::SILU) cs_up[j] = scale ? scale[p.up_off + col0 + j] : 1.f;
+    for (int j = 0; j < G::NI; ++j) {
+      sc.cs[j] = scale[col0 + j];
+      if constexpr (G::SILU) sc.cs_up[j] = scale[p.up_off + col0 + j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < G::NI; ++j) {
+      sc.cs[j] = 1.f;
+      if constexpr (G::SILU) sc.cs_up[j] = 1.f;
+    }
   }
-  float rs[MBE][4];   // fp8 activations: per-row scale of the A row each output row came from
 #pragma unroll
   for (int i = 0; i < MBE; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = tc.row0 + wm * 16 * MBE + i * 16 + lq * 4 + r;
-      rs[i][r] = a_scale && row < tc.row_end ? a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
-    }
+    for (int r = 0; r < 4; ++r)
+      src_row[i][r] = min(tc.row0 + wm * 16 * MBE + i * 16 + (lane >> 4) * 4 + r, tc.row_end - 1);
+  if (a_scale && p.a_rows) {
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) src_row[i][r] = p.a_rows[src_row[i][r]];
+  }
+}
+
+template <class G, int MBE>
+__device__ __forceinline__ void epi_load_scales_2(const float* a_scale, EpiScales<G, MBE>& sc,
+                                                  const int (&src_row)[MBE][4]) {
+  if (a_scale) {
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc.rs[i][r] = a_scale[src_row[i][r]];
+  } else {
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc.rs[i][r] = 1.f;
+  }
+}
+
+template <class G, int EPI, int MBE>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc, f32x4_t (&acc)[MBE][G::NB], int wm,
+                                         int wn, int lane, const EpiScales<G, MBE>& sc) {
+  const int lq = lane >> 4;
+  const int col0 = epi_col0<G, MBE>(tc, wn, lane);
+  const auto& cs = sc.cs;
+  const auto& cs_up = sc.cs_up;
+  const auto& rs = sc.rs;
 #pragma unroll
   for (int i = 0; i < MBE; ++i) {
 #pragma unroll
@@ -322,6 +375,16 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
       }
     }
   }
+}
+
+template <class G, int EPI, int MBE>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc, f32x4_t (&acc)[MBE][G::NB], int wm,
+                                         int wn, int lane, const float* scale, const float* a_scale) {
+  EpiScales<G, MBE> sc;
+  int src_row[MBE][4];
+  epi_load_scales_1<G, MBE>(p, tc, wm, wn, lane, scale, a_scale, sc, src_row);
+  epi_load_scales_2<G, MBE>(a_scale, sc, src_row);
+  epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, sc);
 }
 
 // Issues one K slab of A and B straight into LDS: each wave instruction fills one
@@ -722,11 +785,25 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    // e4m3: the epilogue's scales are loaded here, around the first slab's DMA, instead of after
+    // the K loop (the activation scale is two dependent loads, row map then scale, ~5 us of a
+    // ~60 us tile at the epilogue): the row map before the DMA, the scales after it, so their
+    // round trip overlaps the DMA's.  24 VGPRs held through the loop.
+    EpiScales<G, MBE> sc;
+    int src_row[MBE][4];
+    if constexpr (FP8) epi_load_scales_1<G, MBE>(p, tc, wm, wn, lane, scale, p.a_scale, sc, src_row);
     // slab 0 into (A0, B0), B of slab 1 into B1 (the prefix in B2 is no longer read: every
     // thread finished decode_tile before the barrier below, and B2's first load comes after it)
     issue_ab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, 0, 0);
     issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
+    if constexpr (FP8) epi_load_scales_2<G, MBE>(p.a_scale, sc, src_row);
     pp_wait_vm0();
+    if constexpr (FP8) {   // keeps the loads here: the compiler would otherwise sink them to their use
+      for (auto& x : sc.cs) asm volatile("" ::"v"(x));
+      for (auto& x : sc.cs_up) asm volatile("" ::"v"(x));
+      for (auto& row : sc.rs)
+        for (auto& x : row) asm volatile("" ::"v"(x));
+    }
     pp_barrier();
     if (grp == 1) pp_barrier();
     PpFrags<FP8, G, MBE> fr;
@@ -767,7 +844,8 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
 #undef EIMOE_PP3_HALF
     if (grp == 0) pp_barrier();   // matches group 1's late start
     pp_wait_vm0();                // the clamped loads near the end land before the LDS is released
-    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale, FP8 ? p.a_scale : nullptr);
+    if constexpr (FP8) epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, sc);
+    else epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr, nullptr);
   });
 }
 

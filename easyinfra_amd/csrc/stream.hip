@@ -265,13 +265,20 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
 #pragma unroll
   for (int f = 0; f < NFRAG; ++f)
     cs[f] = FP8 ? p.b_scale[static_cast<long long>(expert) * p.nb_rows + wrow[f]] : 1.f;
+  // rows past the segment read the last row's scale (never stored): no per-row branch, so the
+  // row-map loads issue back to back, then the scale loads (not one dependent pair per row)
+  int src_row[MBLK][4];
 #pragma unroll
   for (int m = 0; m < MBLK; ++m)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = row0 + m * 16 + lq * 4 + r;
-      rsv[m][r] = FP8 && row < row_end ? p.a_scale[p.a_rows ? p.a_rows[row] : row] : 1.f;
+      const int row = min(row0 + m * 16 + lq * 4 + r, row_end - 1);
+      src_row[m][r] = FP8 ? (p.a_rows ? p.a_rows[row] : row) : 0;
     }
+#pragma unroll
+  for (int m = 0; m < MBLK; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rsv[m][r] = FP8 ? p.a_scale[src_row[m][r]] : 1.f;
 #pragma unroll
   for (int m = 0; m < MBLK; ++m) {
 #pragma unroll
