@@ -94,6 +94,28 @@ struct TileCoord {
   int expert, row0, row_end, n_tile, split;
 };
 
+// Tile `rest` of a split given its segment (clamped rows [seg_r0, seg_r1)) and the segment's first
+// m-tile over all segments (pref).  Groups of GM m-tiles sweep the n-tiles together (sharing each
+// weight panel through L2); the last group takes the segment's remaining 1..2*GM-1 m-tiles, so a
+// short remainder tile shares the panels of the group before it instead of reading them alone.
+template <int BM, int GM>
+__device__ __forceinline__ void place_tile(const GemmArgs& p, int seg, int seg_r0, int seg_r1, int pref, int rest,
+                                           int n_tiles, int split, TileCoord& tc) {
+  const int local = rest - pref * n_tiles;
+  const int mt_s = (seg_r1 - seg_r0 + BM - 1) / BM;
+  const int n_grp = max(1, mt_s / GM);
+  const int grp = min(local / (GM * n_tiles), n_grp - 1);
+  const int gm = grp < n_grp - 1 ? GM : mt_s - grp * GM;
+  const int r_in = local - grp * GM * n_tiles;
+  const int n_tile = r_in / gm;
+  const int m_tile = grp * GM + (r_in - n_tile * gm);
+  tc.row0 = uniform(seg_r0 + m_tile * BM);
+  tc.row_end = uniform(min(seg_r0 + m_tile * BM + BM, seg_r1));
+  tc.expert = uniform(seg % p.e_mod);
+  tc.split = uniform(split);
+  tc.n_tile = uniform(n_tile);
+}
+
 // Decodes this workgroup's tile; returns false (uniformly) if the workgroup has no work.
 // Must be reached by every thread of the workgroup (contains a barrier).
 template <int BM, int OUT_BN, int GM>
@@ -136,24 +158,49 @@ __device__ __forceinline__ bool decode_tile(const GemmArgs& p, int* s_pref, Tile
     else hi = mid - 1;
   }
   const int seg = lo;
-  const int local = rest - s_pref[seg] * n_tiles;
-  const int mt_s = s_pref[seg + 1] - s_pref[seg];
-  // Groups of GM m-tiles sweep the n-tiles together (sharing each weight panel through L2); the
-  // last group takes the segment's remaining 1..2*GM-1 m-tiles, so a short remainder tile
-  // shares the panels of the group before it instead of reading them from HBM alone.
-  const int n_grp = max(1, mt_s / GM);
-  const int grp = min(local / (GM * n_tiles), n_grp - 1);
-  const int gm = grp < n_grp - 1 ? GM : mt_s - grp * GM;
-  const int r_in = local - grp * GM * n_tiles;
-  tc.n_tile = r_in / gm;
-  const int m_tile = grp * GM + (r_in - tc.n_tile * gm);
   const int seg_r0 = min(max(p.seg_off[seg], 0), p.max_rows);
   const int seg_r1 = min(max(p.seg_off[seg + 1], seg_r0), p.max_rows);
-  tc.row0 = uniform(seg_r0 + m_tile * BM);
-  tc.row_end = uniform(min(seg_r0 + m_tile * BM + BM, seg_r1));
-  tc.expert = uniform(seg % p.e_mod);
-  tc.split = uniform(split);
-  tc.n_tile = uniform(tc.n_tile);
+  place_tile<BM, GM>(p, seg, seg_r0, seg_r1, s_pref[seg], rest, n_tiles, split, tc);
+  return true;
+}
+
+// Tile schedule of a launch with at most 64 segments, held in registers (lane s: segment s):
+// a persistent workgroup decodes each of its tiles with a ballot and lane reads, no memory access.
+struct RegSched {
+  int r0, r1, incl;                         // lane s: clamped rows, inclusive m-tile prefix
+  int n_tiles, per_split, total, per_xcd;   // uniform
+};
+
+template <int BM, int OUT_BN>
+__device__ __forceinline__ RegSched reg_sched(const GemmArgs& p, int lane) {
+  RegSched s;
+  s.r0 = 0;
+  s.r1 = 0;
+  if (lane < p.S) {
+    s.r0 = min(max(p.seg_off[lane], 0), p.max_rows);
+    s.r1 = min(max(p.seg_off[lane + 1], s.r0), p.max_rows);
+  }
+  s.incl = wave_incl_scan((s.r1 - s.r0 + BM - 1) / BM);
+  s.n_tiles = p.N / OUT_BN;
+  s.per_split = uniform(__shfl(s.incl, 63, 64)) * s.n_tiles;
+  s.total = s.per_split * p.k_split;
+  s.per_xcd = (s.total + kNumXcd - 1) / kNumXcd;
+  return s;
+}
+
+// Coordinates of logical tile `logical` (uniform); false past the end.
+template <int BM, int GM>
+__device__ __forceinline__ bool reg_decode(const GemmArgs& p, const RegSched& s, int logical, TileCoord& tc) {
+  if (logical >= s.total) return false;
+  const int split = logical / s.per_split;
+  const int rest = logical - split * s.per_split;
+  const int q = rest / s.n_tiles;   // m-tile over all segments
+  // the first lane whose inclusive prefix passes q holds the segment (lanes past S hold the total)
+  const int seg = uniform(static_cast<int>(__popcll(__ballot(s.incl <= q))));
+  const int seg_r0 = __builtin_amdgcn_readlane(s.r0, seg);
+  const int seg_r1 = __builtin_amdgcn_readlane(s.r1, seg);
+  const int pref = __builtin_amdgcn_readlane(s.incl, seg) - (seg_r1 - seg_r0 + BM - 1) / BM;
+  place_tile<BM, GM>(p, seg, seg_r0, seg_r1, pref, rest, s.n_tiles, split, tc);
   return true;
 }
 
@@ -284,10 +331,13 @@ __device__ __forceinline__ int epi_col0(const TileCoord& tc, int wn, int lane) {
 // activation scales of the mapped rows.
 // The null tests sit outside the loops: tested per element, they split the loads into one
 // block each, and the wait inserted at every block waited for the loads in flight before it.
+// mbe: the tile's 16-row fragments per wave (MBE for a tile of the full MBE class; a persistent
+// kernel loads the scales of its next tile, whose class it knows only at run time, into the
+// full-size arrays: rows past the tile's are clamped to its last).
 template <class G, int MBE>
 __device__ __forceinline__ void epi_load_scales_1(const GemmArgs& p, const TileCoord& tc, int wm, int wn, int lane,
                                                   const float* scale, const float* a_scale, EpiScales<G, MBE>& sc,
-                                                  int (&src_row)[MBE][4]) {
+                                                  int (&src_row)[MBE][4], int mbe = MBE) {
   const int col0 = epi_col0<G, MBE>(tc, wn, lane);
   if (scale) {
 #pragma unroll
@@ -306,7 +356,7 @@ __device__ __forceinline__ void epi_load_scales_1(const GemmArgs& p, const TileC
   for (int i = 0; i < MBE; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      src_row[i][r] = min(tc.row0 + wm * 16 * MBE + i * 16 + (lane >> 4) * 4 + r, tc.row_end - 1);
+      src_row[i][r] = min(tc.row0 + wm * 16 * mbe + i * 16 + (lane >> 4) * 4 + r, tc.row_end - 1);
   if (a_scale && p.a_rows) {
 #pragma unroll
     for (int i = 0; i < MBE; ++i)
@@ -331,9 +381,10 @@ __device__ __forceinline__ void epi_load_scales_2(const float* a_scale, EpiScale
   }
 }
 
-template <class G, int EPI, int MBE>
+template <class G, int EPI, int MBE, int MBS>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc, f32x4_t (&acc)[MBE][G::NB], int wm,
-                                         int wn, int lane, const EpiScales<G, MBE>& sc) {
+                                         int wn, int lane, const EpiScales<G, MBS>& sc) {
+  static_assert(MBS >= MBE, "scales of every fragment row");
   const int lq = lane >> 4;
   const int col0 = epi_col0<G, MBE>(tc, wn, lane);
   const auto& cs = sc.cs;
@@ -733,8 +784,102 @@ __device__ __forceinline__ void pp_mma(f32x4_t (&acc)[MBE][G::NB], const PpFrags
   }
 }
 
+// The five LDS stages of the ping-pong kernels: A in two, B in three (5 x 32 KiB).
+struct PpStages {
+  uint16_t *a0, *a1, *b0, *b1, *b2;
+};
+
+// Operand windows and per-lane B offsets of one 256x256 ping-pong tile.
+template <class G, int EB, int FR = 16>
+struct PpOperands {
+  static constexpr int B_PW = 256 / 8 / G::NW;
+  BufRef rA, rB;
+  uint32_t b_voff[B_PW];
+  __device__ __forceinline__ PpOperands(const GemmArgs& p, const TileCoord& tc, int wave, int lane) {
+    const long long k0 = static_cast<long long>(tc.split) * p.K;
+    // uniform by construction, taken from the first lane so that the compiler keeps them in
+    // SGPRs: in the persistent kernel's tile loop it could not prove it and wrapped every
+    // buffer load in a readfirstlane loop (measured: MFMA busy 63 % against 79 %)
+    rA = BufRef{uniform(static_cast<const uint8_t*>(p.a) + k0 * EB), uniform((p.a_rows_cap * p.lda - k0) * EB)};
+    rB = BufRef{uniform(expert_weights(p, tc.expert, EB) + k0 * EB), uniform((p.b_estride - k0) * EB)};
+#pragma unroll
+    for (int i = 0; i < B_PW; ++i) {
+      const int R = (wave * B_PW + i) * 8 + (lane >> 3);
+      const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
+      b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb * EB + (((lane & 7) ^ swz(R)) << 4));
+    }
+  }
+};
+
+// The K loop of one tile, from the first slab's data in (A0, B0) and B of the second slab in B1
+// (waited for and published by the caller's barrier) to every wave's last LDS read.  Group 1
+// enters one phase late; both groups execute 4*KT + 2 barriers including the caller's one.
 // FP8: e4m3 activations and weights (W8A8); an LDS row is 128 bytes either way (64 bf16 or 128
 // e4m3 of K per slab), so the DMA, the swizzle and the stages are the same bytes.
+template <bool FP8, class G, int MBE, int A_CNT, int A_PW, int B_PW>
+__device__ __forceinline__ void pp3_kloop(f32x4_t (&acc)[MBE][G::NB], const BufRef& rA, const BufRef& rB,
+                                          const uint32_t (&a_voff)[A_PW], const uint32_t (&b_voff)[B_PW], int KT,
+                                          int wave, int lane, const PpStages& st) {
+  constexpr int BK = G::BK;
+  constexpr int NW = G::NW;
+  const int grp = wave >> 2;
+  const int wm = wave % 4;
+  const int wn = wave / 4;
+  uint16_t* const sA0 = st.a0;
+  uint16_t* const sA1 = st.a1;
+  uint16_t* const sB0 = st.b0;
+  uint16_t* const sB1 = st.b1;
+  uint16_t* const sB2 = st.b2;
+  if (grp == 1) pp_barrier();
+  PpFrags<FP8, G, MBE> fr;
+  // The phase's DMA goes ahead of its fragment reads for bf16, after them for e4m3 (A/B on one
+  // box: bf16 prefill 4.47 vs 4.50 ms; W8A8 prefill 2.76 vs 2.65 ms).
+#define EIMOE_PP3_HALF(SA, SB, KK, DMA)                   \
+  if constexpr (!FP8) DMA;                                \
+  pp_read<FP8, G, MBE, KK>(fr, SA, SB, wm, wn, lane);     \
+  if constexpr (FP8) {                                    \
+    pin_issue();                                          \
+    DMA;                                                  \
+    pin_issue();                                          \
+  }                                                       \
+  pp_wait_lgkm0();                                        \
+  if (KK == 1 && grp == 1) pp_wait_vm4();                 \
+  pp_barrier();                                           \
+  pp_mma<FP8, G, MBE, KK>(acc, fr);                       \
+  if (KK == 1 && grp == 0) pp_wait_vm4();                 \
+  pp_barrier();
+  // slab kt + J: read (SA, SB); load A(kt+J+1) into SAN and B(kt+J+2) into SBN (clamped to
+  // the last slab near the end: those stages are not read again)
+#define EIMOE_PP3_SLAB(J, SA, SB, SAN, SBN)                                                              \
+  if (kt + J < KT) {                                                                                     \
+    EIMOE_PP3_HALF(SA, SB, 0, (issue_a_dma<A_CNT, NW>(rA, a_voff, SAN, wave, min(kt + J + 1, KT - 1) * BK * 2))) \
+    EIMOE_PP3_HALF(SA, SB, 1,                                                                            \
+                   (issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, 0,                  \
+                                              min(kt + J + 2, KT - 1) * BK * 2)))                        \
+  }
+  for (int kt = 0; kt < KT; kt += 6) {
+    EIMOE_PP3_SLAB(0, sA0, sB0, sA1, sB2)
+    EIMOE_PP3_SLAB(1, sA1, sB1, sA0, sB0)
+    EIMOE_PP3_SLAB(2, sA0, sB2, sA1, sB1)
+    EIMOE_PP3_SLAB(3, sA1, sB0, sA0, sB2)
+    EIMOE_PP3_SLAB(4, sA0, sB1, sA1, sB0)
+    EIMOE_PP3_SLAB(5, sA1, sB2, sA0, sB1)
+  }
+#undef EIMOE_PP3_SLAB
+#undef EIMOE_PP3_HALF
+  if (grp == 0) pp_barrier();   // matches group 1's late start: every wave has read its last slab
+}
+
+// Pins values in registers at this point (an empty asm that takes them as operands): loads
+// issued early then complete here instead of being sunk by the compiler to their first use.
+template <class G, int MBE>
+__device__ __forceinline__ void pin_scales(EpiScales<G, MBE>& sc) {
+  for (auto& x : sc.cs) asm volatile("" ::"v"(x));
+  for (auto& x : sc.cs_up) asm volatile("" ::"v"(x));
+  for (auto& row : sc.rs)
+    for (auto& x : row) asm volatile("" ::"v"(x));
+}
+
 template <int EPI, int GM, bool FP8 = false>
 __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
   using G = Geo<256, 256, 4, 2, EPI>;
@@ -751,27 +896,16 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) uint16_t sB0[256 * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sB1[256 * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sB2[256 * BK];
+  const PpStages st{sA0, sA1, sB0, sB1, sB2};
 
   TileCoord tc;
   if (!decode_tile<256, G::OUT_BN, GM>(p, reinterpret_cast<int*>(sB2), tc)) return;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = wave >> 2;
-  const int lrow = lane >> 3;
-  const long long k0 = static_cast<long long>(tc.split) * p.K;
-
-  const BufRef rA{static_cast<const uint8_t*>(p.a) + k0 * EB, (p.a_rows_cap * p.lda - k0) * EB};
   uint32_t a_voff[A_PW];
   a_offsets<A_PW, NW>(p, tc, wave, lane, EB, a_voff);
-  const BufRef rB{expert_weights(p, tc.expert, EB) + k0 * EB, (p.b_estride - k0) * EB};
-  uint32_t b_voff[B_PW];
-#pragma unroll
-  for (int i = 0; i < B_PW; ++i) {
-    const int R = (wave * B_PW + i) * 8 + lrow;
-    const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
-    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb * EB + (((lane & 7) ^ swz(R)) << 4));
-  }
+  const PpOperands<G, EB> op(p, tc, wave, lane);
   const float* scale = FP8 ? p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows : nullptr;
 
   const int wm = wave % 4;
@@ -794,59 +928,125 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
     if constexpr (FP8) epi_load_scales_1<G, MBE>(p, tc, wm, wn, lane, scale, p.a_scale, sc, src_row);
     // slab 0 into (A0, B0), B of slab 1 into B1 (the prefix in B2 is no longer read: every
     // thread finished decode_tile before the barrier below, and B2's first load comes after it)
-    issue_ab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, 0, 0);
-    issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
+    issue_ab_dma<A_CNT, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB0, wave, 0, 0);
+    issue_ab_dma<0, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
     if constexpr (FP8) epi_load_scales_2<G, MBE>(p.a_scale, sc, src_row);
     pp_wait_vm0();
-    if constexpr (FP8) {   // keeps the loads here: the compiler would otherwise sink them to their use
-      for (auto& x : sc.cs) asm volatile("" ::"v"(x));
-      for (auto& x : sc.cs_up) asm volatile("" ::"v"(x));
-      for (auto& row : sc.rs)
-        for (auto& x : row) asm volatile("" ::"v"(x));
-    }
+    if constexpr (FP8) pin_scales(sc);   // the compiler would otherwise sink the loads to their use
     pp_barrier();
-    if (grp == 1) pp_barrier();
-    PpFrags<FP8, G, MBE> fr;
-    // The phase's DMA goes ahead of its fragment reads for bf16, after them for e4m3 (A/B on one
-    // box: bf16 prefill 4.47 vs 4.50 ms; W8A8 prefill 2.76 vs 2.65 ms).
-#define EIMOE_PP3_HALF(SA, SB, KK, DMA)                   \
-    if constexpr (!FP8) DMA;                              \
-    pp_read<FP8, G, MBE, KK>(fr, SA, SB, wm, wn, lane);   \
-    if constexpr (FP8) {                                  \
-      pin_issue();                                        \
-      DMA;                                                \
-      pin_issue();                                        \
-    }                                                     \
-    pp_wait_lgkm0();                                      \
-    if (KK == 1 && grp == 1) pp_wait_vm4();               \
-    pp_barrier();                                         \
-    pp_mma<FP8, G, MBE, KK>(acc, fr);                     \
-    if (KK == 1 && grp == 0) pp_wait_vm4();               \
-    pp_barrier();
-    // slab kt + J: read (SA, SB); load A(kt+J+1) into SAN and B(kt+J+2) into SBN (clamped to
-    // the last slab near the end: those stages are not read again)
-#define EIMOE_PP3_SLAB(J, SA, SB, SAN, SBN)                                                              \
-    if (kt + J < KT) {                                                                                   \
-      EIMOE_PP3_HALF(SA, SB, 0, (issue_a_dma<A_CNT, NW>(rA, a_voff, SAN, wave, min(kt + J + 1, KT - 1) * BK * 2))) \
-      EIMOE_PP3_HALF(SA, SB, 1,                                                                          \
-                     (issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, 0,                \
-                                                min(kt + J + 2, KT - 1) * BK * 2)))                      \
-    }
-    for (int kt = 0; kt < KT; kt += 6) {
-      EIMOE_PP3_SLAB(0, sA0, sB0, sA1, sB2)
-      EIMOE_PP3_SLAB(1, sA1, sB1, sA0, sB0)
-      EIMOE_PP3_SLAB(2, sA0, sB2, sA1, sB1)
-      EIMOE_PP3_SLAB(3, sA1, sB0, sA0, sB2)
-      EIMOE_PP3_SLAB(4, sA0, sB1, sA1, sB0)
-      EIMOE_PP3_SLAB(5, sA1, sB2, sA0, sB1)
-    }
-#undef EIMOE_PP3_SLAB
-#undef EIMOE_PP3_HALF
-    if (grp == 0) pp_barrier();   // matches group 1's late start
+    pp3_kloop<FP8, G, MBE, A_CNT>(acc, op.rA, op.rB, a_voff, op.b_voff, KT, wave, lane, st);
     pp_wait_vm0();                // the clamped loads near the end land before the LDS is released
     if constexpr (FP8) epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, sc);
     else epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr, nullptr);
   });
+}
+
+// Fragment rows per wave (MBE) of a tile of `rows` rows: the height classes of by_height for the
+// 256x256 tile (64, 128 or 256 rows).
+__device__ __forceinline__ int pp_mbe(int rows) { return rows <= 64 ? 1 : rows <= 128 ? 2 : 4; }
+
+// The ping-pong kernel as a persistent loop over tiles, for launches of at most 64 segments.
+// One workgroup per CU (the LDS allows no more); workgroup b walks the tiles b / 8, b / 8 +
+// grid / 8, ... of XCD b % 8's share, the XCD-major order of the one-tile-per-workgroup launch,
+// so the tiles running at one time on an XCD still share weight panels in its L2.  Per tile the
+// one-tile-per-workgroup kernel spends ~1.5 us decoding the schedule, ~2.5 us waiting for its
+// first slabs and ~1.7 us between workgroups (timestamped per tile on the Mixtral-8x7B
+// prefill); here the schedule lives in registers (reg_sched), the next tile's row map is
+// loaded during the first slab of the current one, and the next tile's first DMA (and e4m3
+// scales) is issued before the current tile's epilogue, into each wave's own LDS blocks, which
+// no wave reads any more once the K loop's last barrier has passed.  Every workgroup's loop is
+// bounded by its share of the tiles.  Same tiles, DMA and accumulation order as
+// grouped_gemm_pp3_kernel: bit-identical results.
+template <int EPI, int GM, bool FP8 = false>
+__global__ void __launch_bounds__(512) grouped_gemm_pp3p_kernel(GemmArgs p) {
+  using G = Geo<256, 256, 4, 2, EPI>;
+  constexpr int BK = G::BK;
+  constexpr int EB = FP8 ? 1 : 2;
+  constexpr int NW = G::NW;
+  constexpr int A_PW = 256 / 8 / G::NW;
+  constexpr int B_PW = 256 / 8 / G::NW;
+  constexpr int MB = G::MB;
+  static_assert(B_PW == 4, "the slab-end wait is vmcnt(B_PW)");
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[256 * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[256 * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[256 * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[256 * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB2[256 * BK];
+  const PpStages st{sA0, sA1, sB0, sB1, sB2};
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave % 4;
+  const int wn = wave / 4;
+  const int KT = p.K * EB / (BK * 2);
+  const RegSched rsch = reg_sched<256, G::OUT_BN>(p, lane);
+  const int xcd = blockIdx.x % kNumXcd;
+  const int stride = gridDim.x / kNumXcd;   // the launch rounds the grid to whole XCD rounds
+  auto logical_of = [&](int sl) { return sl < rsch.per_xcd ? xcd * rsch.per_xcd + sl : rsch.total; };
+  int slot = blockIdx.x / kNumXcd;
+  TileCoord tc;
+  if (!reg_decode<256, GM>(p, rsch, logical_of(slot), tc)) return;
+
+  // first tile: its row map, scales and first slabs (every A block: a short tile's extra rows
+  // repeat its last row and are not read)
+  uint32_t a_voff[A_PW];
+  a_offsets<A_PW, NW>(p, tc, wave, lane, EB, a_voff);
+  EpiScales<G, MB> sc;
+  {
+    const PpOperands<G, EB> op(p, tc, wave, lane);
+    const float* scale = FP8 ? p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows : nullptr;
+    int src_row[MB][4];
+    if constexpr (FP8) epi_load_scales_1<G, MB>(p, tc, wm, wn, lane, scale, p.a_scale, sc, src_row, pp_mbe(tc.row_end - tc.row0));
+    issue_ab_dma<A_PW, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB0, wave, 0, 0);
+    issue_ab_dma<0, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
+    if constexpr (FP8) epi_load_scales_2<G, MB>(p.a_scale, sc, src_row);
+  }
+  for (;;) {
+    TileCoord tn;
+    const bool more = reg_decode<256, GM>(p, rsch, logical_of(slot + stride), tn);
+    // The lane index, opaque to the compiler once per tile: otherwise it hoists the lane address
+    // arithmetic of all three height classes out of the tile loop, all live at once (256 VGPRs
+    // and spills against 196 for one tile per workgroup).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    by_height<256, MB, A_PW>(tc.row_end - tc.row0, [&]<int MBE>() {
+      const int lane = ln;
+      constexpr int A_CNT = A_PW * MBE / MB;
+      f32x4_t acc[MBE][G::NB];
+#pragma unroll
+      for (int i = 0; i < MBE; ++i)
+#pragma unroll
+        for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const PpOperands<G, EB> op(p, tc, wave, lane);
+      pp_wait_vm0();   // this tile's first slabs and scales (and the previous tile's stores)
+      if constexpr (FP8) pin_scales(sc);
+      pp_barrier();
+      // the next tile's row map: in flight during the first slab, whose end wait covers it
+      uint32_t an_voff[A_PW];
+      if (more) a_offsets<A_PW, NW>(p, tn, wave, lane, EB, an_voff);
+      pp3_kloop<FP8, G, MBE, A_CNT>(acc, op.rA, op.rB, a_voff, op.b_voff, KT, wave, lane, st);
+      pp_wait_vm0();   // this wave's clamped loads have landed in its own LDS blocks
+      EpiScales<G, MB> sn;
+      if (more) {
+        const PpOperands<G, EB> on(p, tn, wave, lane);
+        const float* scale_n = FP8 ? p.b_scale + static_cast<long long>(tn.expert) * p.nb_rows : nullptr;
+        int src_row[MB][4];
+        if constexpr (FP8)
+          epi_load_scales_1<G, MB>(p, tn, wm, wn, lane, scale_n, p.a_scale, sn, src_row, pp_mbe(tn.row_end - tn.row0));
+        issue_ab_dma<A_PW, B_PW, NW>(on.rA, on.rB, an_voff, on.b_voff, sA0, sB0, wave, 0, 0);
+        issue_ab_dma<0, B_PW, NW>(on.rA, on.rB, an_voff, on.b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
+        if constexpr (FP8) epi_load_scales_2<G, MB>(p.a_scale, sn, src_row);
+#pragma unroll
+        for (int i = 0; i < A_PW; ++i) a_voff[i] = an_voff[i];
+      }
+      if constexpr (FP8) epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, sc);
+      else epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr, nullptr);
+      if constexpr (FP8) sc = sn;
+    });
+    if (!more) break;
+    tc = tn;
+    slot += stride;
+  }
 }
 
 template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
@@ -1034,6 +1234,16 @@ static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
   long long grid = (total + kNumXcd - 1) / kNumXcd * kNumXcd;
   if (grid < kNumXcd) grid = kNumXcd;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
+  if (p.S <= 64) {
+    // persistent: one workgroup per CU at most (the grid stays a whole number of XCD rounds).
+    // Against one tile per workgroup (A/B on one box): Mixtral-8x7B W8A8 gate/up 1524 -> 1485 us
+    // under counters, layers within 0-1 % (the bf16 GEMMs run at the chip's power-limited clock
+    // either way, so hiding the per-tile latencies buys them nothing).
+    const long long pgrid = std::min<long long>(grid, kNumCu);
+    hipLaunchKernelGGL((grouped_gemm_pp3p_kernel<EPI, GMX, FP8>), dim3(static_cast<unsigned>(pgrid)), dim3(512), 0, s,
+                       p);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((grouped_gemm_pp3_kernel<EPI, GMX, FP8>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, s,
                      p);
   return hipGetLastError();
