@@ -408,7 +408,7 @@ def main():
     gu_flops = 4.0 * A * H * I
     gu_ms = stages["gate_up_silu"]
     achieved = gu_flops / (gu_ms * 1e-3) / 1e12
-    roof = {"bound": "mfma", "kernel": "grouped_gemm_pp3_kernel<2,4,false> (256x256 bf16 gate/up + SiLU*mul)",
+    roof = {"bound": "mfma", "kernel": "grouped_gemm_pp3p_kernel<2,8,false> (256x256 bf16 gate/up + SiLU*mul, persistent)",
             "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic_from_profiles("gate_up_silu_prefill"),
             "flops_per_launch": gu_flops, "mean_launch_ms": round(gu_ms, 4)}

@@ -1222,10 +1222,10 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
 // loads hoisted, gate/up 2.32 -> 1.95 ms and down (K split 2) 1.08 -> 0.89 ms against the
 // lock-step kernel, A/B on one box).  W8A16 keeps the lock-step kernel (its B goes through
 // registers for the conversion).
-// Tile grouping depth 4.  16 measured 3 % faster on the bare Mixtral prefill GEMMs (gate/up
-// 3.16 vs 3.25 ms) but not on whole layers (Mixtral 8192 tokens 4.94-4.98 vs 4.92-4.95 ms;
-// DeepSeek-V2-Lite and Qwen3 within noise), so the layer's figure decides.
-template <int EPI, bool FP8 = false, int GMX = 4>
+// Tile grouping depth 8: on the current kernels (persistent tile walk, hardware-reciprocal SiLU)
+// depth 8 and 16 both run the Mixtral-8x7B 8192-token layer ~1 % faster than 4 (4.25 vs 4.29 ms,
+// W8A8 2.40-2.42 vs 2.43-2.44 ms; DeepSeek-V2-Lite within noise, two repeats on one box).
+template <int EPI, bool FP8 = false, int GMX = 8>
 static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
   constexpr int OUT_BN = epi_silu(EPI) ? 128 : 256;
   const int n_tiles = p.N / OUT_BN;
