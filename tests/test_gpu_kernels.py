@@ -333,6 +333,42 @@ def test_down_gemm(dev, tile, k_split):
         torch.testing.assert_close(y[a:b], ref, rtol=1e-4, atol=1e-4)
 
 
+# The 256x256 GEMM runs as a persistent kernel for launches of at most 64 segments and as one
+# tile per workgroup beyond that.  Padding the same segments with empty ones switches kernels
+# without changing any tile (empty segments own no tiles), so the two must agree bit for bit:
+# full, half (129 rows) and quarter (1, 44, 64 rows) height tiles, gathered rows, split K, and
+# enough tiles that every persistent workgroup walks several.
+@pytest.mark.parametrize("w8a8", [False, True])
+def test_persistent_gemm_bit_exact_with_one_tile_kernel(dev, w8a8):
+    g = torch.Generator().manual_seed(77 + w8a8)
+    H, I, T = 512, 512, 600   # down K split 2 keeps whole 128-byte e4m3 slabs
+    counts = [300, 0, 1, 513, 64, 129, 700, 44]
+    E = len(counts)
+    off, off_t = _segments(counts)
+    off_pad = np.concatenate([off, np.full(64, off[-1], dtype=np.int32)])
+    assert len(off_pad) - 1 > 64
+    off_t, off_pad_t = off_t.to(dev), torch.as_tensor(off_pad).to(dev)
+    rows = int(off[-1])
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32).to(dev)
+    w_gu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    w_d = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    hs = torch.randn(rows, I, generator=g).to(torch.bfloat16).to(dev)
+    if w8a8:
+        xq, sx = ops.quantize_rows_fp8(x)
+        qgu, sgu = ops.quantize_weights_fp8(w_gu)
+        qd, sd = ops.quantize_weights_fp8(w_d)
+        hq, sh = ops.quantize_rows_fp8(hs)
+        gu = lambda o: ops.gemm_gate_up_silu_w8a8(xq, sx, qgu, sgu, o, rows, a_rows=a_rows, e_mod=E, tile=1)
+        dn = lambda o, ks: ops.gemm_down_w8a8(hq, sh, qd, sd, o, rows, k_split=ks, e_mod=E, tile=1)
+    else:
+        gu = lambda o: ops.gemm_gate_up_silu(x, w_gu, o, rows, a_rows=a_rows, e_mod=E, tile=1)
+        dn = lambda o, ks: ops.gemm_down(hs, w_d, o, rows, out_dtype=torch.float32, k_split=ks, e_mod=E, tile=1)
+    assert torch.equal(cpu(gu(off_t)), cpu(gu(off_pad_t)))
+    for ks in (1, 2):
+        assert torch.equal(cpu(dn(off_t, ks)), cpu(dn(off_pad_t, ks)))
+
+
 # The weight-streaming kernel (tile 5) picks its column width (8/4/2 fragments), its K split
 # over waves and its register ring depth (2 or 1) from the shapes, or, for grids this small,
 # the short-stream mode (K split over 4 or 8 waves, at most 4 k-steps each, all in flight:
