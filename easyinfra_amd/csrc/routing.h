@@ -88,15 +88,15 @@ __device__ __forceinline__ void route_rows(const float* __restrict__ logits, int
     for (int r = 0; r < k; ++r) {
       float bv = NEG_INF;
       int bi = 0x7fffffff;
+      // Selects, no branches: written with && / || the compiler made each value a divergent
+      // branch block (eight per round at 128 experts), ~0.65 us per pick (timestamped: top-8 of
+      // 128 took 5.3 us of the Qwen3-shape route+align kernel).
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
         const int e = li + j * LPT;
-        if ((avail >> j) & 1u) {
-          if (v[j] > bv || (v[j] == bv && e < bi)) {
-            bv = v[j];
-            bi = e;
-          }
-        }
+        const bool better = (((avail >> j) & 1u) != 0) & ((v[j] > bv) | ((v[j] == bv) & (e < bi)));
+        bv = better ? v[j] : bv;
+        bi = better ? e : bi;
       }
       group_argmax<LPT>(bv, bi);
       if (r == 0) mx = bv;
