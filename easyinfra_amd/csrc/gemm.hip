@@ -18,6 +18,10 @@
 //     so concurrently running workgroups share weight panels (B) and A tiles.
 //   * XCD-aware: workgroups are dispatched round-robin over the 8 XCDs; logical
 //     tile ids are assigned so that consecutive ids run on the same XCD (own L2).
+//   * The 256x256 tile runs persistent for launches of up to 64 segments: one
+//     workgroup per CU walks its XCD's share of the logical tiles, decoding them
+//     from segment bounds held in registers and issuing each next tile's first
+//     loads before the current tile's epilogue.
 //   * Loads are buffer loads through SGPR resources (32-bit per-lane offsets, K
 //     advanced through soffset, out-of-range reads return 0 instead of faulting).
 //     bf16 weights go straight to LDS (buffer_load_dwordx4 ... lds, 1 KiB per wave
