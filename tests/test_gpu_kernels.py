@@ -315,6 +315,34 @@ def test_gate_up_silu(dev, tile, counts):
         torch.testing.assert_close(h[a:b], ref, rtol=1e-2, atol=1e-2)
 
 
+# silu(g) = g * rcp(1 + exp(-g)) in the epilogues (the hardware reciprocal): gate values where
+# exp(-g) overflows (g <= -89: rcp(inf) = 0, h = -0), where the reciprocal is subnormal (g = -88),
+# and where it is 1 (large g).  x rows are one-hot scalings, so g is an exact product of bf16
+# values; h is compared with the float64 silu on those g (bf16 output rounding, tiny values
+# flushed to zero allowed).
+@pytest.mark.parametrize("tile", [1, 2, 5])
+def test_gate_up_silu_extreme_gates(dev, tile):
+    gates = [-200.0, -100.0, -90.0, -88.0, -20.0, -1.0, -1e-3, 0.0, 1e-3, 1.0, 20.0, 88.0, 90.0, 100.0, 200.0, 3.0]
+    H, I, R = 64, 256, 40
+    w = torch.zeros(1, 2 * I, H)
+    for n in range(I):
+        w[0, n, 0] = gates[n % len(gates)]
+        w[0, I + n, 0] = 1.0 + (n % 3)
+    scales = [1.0, 0.5, 2.0, -1.0]
+    x = torch.zeros(R, H)
+    for r in range(R):
+        x[r, 0] = scales[r % len(scales)]
+    x, w = x.to(torch.bfloat16), w.to(torch.bfloat16)
+    off_t = torch.tensor([0, R], dtype=torch.int32)
+    h = ops.gemm_gate_up_silu(x.to(dev), w.to(dev), off_t.to(dev), R, tile=tile)
+    h = cpu(h).double()
+    gu = x.double() @ w[0].double().T
+    g, u = gu[:, :I], gu[:, I:]
+    ref = g * torch.sigmoid(g) * u
+    assert torch.isfinite(h).all()
+    assert ((h - ref).abs() <= 1e-2 * ref.abs() + 1e-6).all(), (h - ref).abs().max()
+
+
 @pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 4), (5, 1), (5, 2), (5, 8)])
 def test_down_gemm(dev, tile, k_split):
     g = torch.Generator().manual_seed(31 + tile * 7 + k_split)
