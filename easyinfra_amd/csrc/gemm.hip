@@ -546,6 +546,17 @@ __device__ __forceinline__ void by_height(int rows, Body&& body) {
   body.template operator()<MB>();
 }
 
+// The MBE by_height picks for a tile of `rows` rows, at run time (a persistent kernel loads its
+// next tile's e4m3 scales before it dispatches on that tile's height).
+template <int BM, int MB, int A_PW>
+__device__ __forceinline__ int mbe_of_rows(int rows) {
+  if constexpr (Heights<MB, A_PW>::kQuarter)
+    if (rows <= BM / 4) return MB / 4;
+  if constexpr (Heights<MB, A_PW>::kHalf)
+    if (rows <= BM / 2) return MB / 2;
+  return MB;
+}
+
 // Per-lane A source offsets for the A_PW blocks of this wave (block i*NW + wave: rows 8 * that
 // + lrow, clamped to the tile's last row), 16-byte chunks pre-swizzled; elem_bytes per element.
 template <int A_PW, int NW>
@@ -758,7 +769,8 @@ __device__ __forceinline__ void pp_read(PpFrags<FP8, G, MBE>& f, const uint16_t*
     const int q = lane >> 4;
     if constexpr (KK == 0) {
 #pragma unroll
-      for (int i = 0; i < MBE; ++i) f.a[i] = frag_fp8(reinterpret_cast<const uint8_t*>(sA), wm * 16 * MBE + i * 16 + lr, q);
+      for (int i = 0; i < MBE; ++i)
+        f.a[i] = frag_fp8(reinterpret_cast<const uint8_t*>(sA), wm * 16 * MBE + i * 16 + lr, q);
     }
 #pragma unroll
     for (int j = 0; j < G::NB / 2; ++j)
@@ -945,10 +957,6 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
   });
 }
 
-// Fragment rows per wave (MBE) of a tile of `rows` rows: the height classes of by_height for the
-// 256x256 tile (64, 128 or 256 rows).
-__device__ __forceinline__ int pp_mbe(int rows) { return rows <= 64 ? 1 : rows <= 128 ? 2 : 4; }
-
 // The ping-pong kernel as a persistent loop over tiles, for launches of at most 64 segments.
 // One workgroup per CU (the LDS allows no more); workgroup b walks the tiles b / 8, b / 8 +
 // grid / 8, ... of XCD b % 8's share, the XCD-major order of the one-tile-per-workgroup launch,
@@ -1000,7 +1008,9 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3p_kernel(GemmArgs p) {
     const PpOperands<G, EB> op(p, tc, wave, lane);
     const float* scale = FP8 ? p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows : nullptr;
     int src_row[MB][4];
-    if constexpr (FP8) epi_load_scales_1<G, MB>(p, tc, wm, wn, lane, scale, p.a_scale, sc, src_row, pp_mbe(tc.row_end - tc.row0));
+    if constexpr (FP8)
+      epi_load_scales_1<G, MB>(p, tc, wm, wn, lane, scale, p.a_scale, sc, src_row,
+                               mbe_of_rows<256, MB, A_PW>(tc.row_end - tc.row0));
     issue_ab_dma<A_PW, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB0, wave, 0, 0);
     issue_ab_dma<0, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
     if constexpr (FP8) epi_load_scales_2<G, MB>(p.a_scale, sc, src_row);
@@ -1036,7 +1046,8 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3p_kernel(GemmArgs p) {
         const float* scale_n = FP8 ? p.b_scale + static_cast<long long>(tn.expert) * p.nb_rows : nullptr;
         int src_row[MB][4];
         if constexpr (FP8)
-          epi_load_scales_1<G, MB>(p, tn, wm, wn, lane, scale_n, p.a_scale, sn, src_row, pp_mbe(tn.row_end - tn.row0));
+          epi_load_scales_1<G, MB>(p, tn, wm, wn, lane, scale_n, p.a_scale, sn, src_row,
+                                   mbe_of_rows<256, MB, A_PW>(tn.row_end - tn.row0));
         issue_ab_dma<A_PW, B_PW, NW>(on.rA, on.rB, an_voff, on.b_voff, sA0, sB0, wave, 0, 0);
         issue_ab_dma<0, B_PW, NW>(on.rA, on.rB, an_voff, on.b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
         if constexpr (FP8) epi_load_scales_2<G, MB>(p.a_scale, sn, src_row);
