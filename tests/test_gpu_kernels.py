@@ -366,14 +366,19 @@ def test_down_gemm(dev, tile, k_split):
 # without changing any tile (empty segments own no tiles), so the two must agree bit for bit:
 # full, half (129 rows) and quarter (1, 44, 64 rows) height tiles, gathered rows, split K, and
 # enough tiles that every persistent workgroup walks several.
-@pytest.mark.parametrize("w8a8", [False, True])
-def test_persistent_gemm_bit_exact_with_one_tile_kernel(dev, w8a8):
-    g = torch.Generator().manual_seed(77 + w8a8)
+@pytest.mark.parametrize("w8a8,n_seg", [(False, 8), (True, 8), (False, 64), (True, 64)])
+def test_persistent_gemm_bit_exact_with_one_tile_kernel(dev, w8a8, n_seg):
+    g = torch.Generator().manual_seed(77 + w8a8 + n_seg)
     H, I, T = 512, 512, 600   # down K split 2 keeps whole 128-byte e4m3 slabs
-    counts = [300, 0, 1, 513, 64, 129, 700, 44]
+    if n_seg == 8:
+        counts = [300, 0, 1, 513, 64, 129, 700, 44]
+    else:   # exactly 64 segments, the persistent kernel's limit (one per lane of its schedule)
+        counts = torch.randint(0, 300, (n_seg,), generator=g).tolist()
+        counts[5] = 0
+        counts[63] = 257
     E = len(counts)
     off, off_t = _segments(counts)
-    off_pad = np.concatenate([off, np.full(64, off[-1], dtype=np.int32)])
+    off_pad = np.concatenate([off, np.full(65 - E if E == 64 else 64, off[-1], dtype=np.int32)])
     assert len(off_pad) - 1 > 64
     off_t, off_pad_t = off_t.to(dev), torch.as_tensor(off_pad).to(dev)
     rows = int(off[-1])
