@@ -135,6 +135,17 @@ __global__ __launch_bounds__(kAlignMbThreads) void align_place_kernel(
 
 size_t align_lds_bytes(int n_loc) { return static_cast<size_t>(align_lds_ints(n_loc)) * sizeof(int); }
 
+hipError_t launch_align_place(const int32_t* ids, int T, int k, int e_lo, int n_loc, int blocks, int chunk,
+                              const int32_t* hist, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
+                              int32_t* sorted_tok, int32_t* pos, hipStream_t s) {
+  if (blocks < 1 || chunk % kAlignMbWaves != 0 || static_cast<long long>(blocks) * n_loc > kAlignMbMaxCells)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(align_place_kernel, dim3(blocks), dim3(kAlignMbThreads),
+                     static_cast<size_t>(kAlignMbWaves + 3) * n_loc * sizeof(int) + sizeof(int), s, ids, T * k, k, e_lo,
+                     n_loc, chunk, hist, counts, offsets, sorted_flat, sorted_tok, pos);
+  return hipGetLastError();
+}
+
 AlignPlan align_plan(int N, int n_loc) {
   AlignPlan pl{};
   if (N < kAlignMbMinIds) return pl;
@@ -160,10 +171,8 @@ hipError_t launch_align(const int32_t* ids, int T, int k, int e_lo, int n_loc, i
                        static_cast<size_t>(kAlignMbWaves) * n_loc * sizeof(int), s, ids, N, e_lo, n_loc, pl.chunk, hist);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(align_place_kernel, dim3(pl.blocks), dim3(kAlignMbThreads),
-                       static_cast<size_t>(kAlignMbWaves + 3) * n_loc * sizeof(int) + sizeof(int), s, ids, N, k, e_lo,
-                       n_loc, pl.chunk, hist, counts, offsets, sorted_flat, sorted_tok, pos);
-    return hipGetLastError();
+    return launch_align_place(ids, T, k, e_lo, n_loc, pl.blocks, pl.chunk, hist, counts, offsets, sorted_flat,
+                              sorted_tok, pos, s);
   }
   const size_t lds = align_lds_bytes(n_loc);
   hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kAlignThreads), lds, s, ids, N, k, e_lo, n_loc, counts,

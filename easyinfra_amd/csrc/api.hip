@@ -191,7 +191,7 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   L.sorted_flat = take(A * 4);
   L.sorted_tok = take(A * 4);
   L.pos = take(A * 4);
-  L.hist = take(align_plan(static_cast<int>(A), n_local).hist_ints * 4);
+  L.hist = take(std::max(align_plan(static_cast<int>(A), n_local).hist_ints, route_hist_ints(T, E, k, n_local)) * 4);
   L.h = take(A * I * hb);
   if (L.h_terms == 2) L.h_lo = take(A * I * 2);
   L.y = take(static_cast<size_t>(L.h_terms) * L.k_split * A * H * elem_size(L.y_dtype));

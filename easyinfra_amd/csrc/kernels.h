@@ -68,9 +68,18 @@ struct AlignPlan {
 AlignPlan align_plan(int N, int n_loc);
 hipError_t launch_align(const int32_t* ids, int T, int k, int e_lo, int n_loc, int32_t* counts, int32_t* offsets,
                         int32_t* sorted_flat, int32_t* sorted_tok, int32_t* pos, int32_t* hist, hipStream_t s);
-// Router then align; one workgroup runs both when route_align_fused() (small batches),
-// otherwise the two kernels above.
+// The many-workgroup align's second pass alone: chunk b = flat ids [b*chunk, (b+1)*chunk)
+// with its per-expert counts in hist[b][n_loc] (chunk a multiple of 4, blocks * n_loc cells
+// at most kAlignMbMaxCells).
+hipError_t launch_align_place(const int32_t* ids, int T, int k, int e_lo, int n_loc, int blocks, int chunk,
+                              const int32_t* hist, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
+                              int32_t* sorted_tok, int32_t* pos, hipStream_t s);
+// Router then align; one workgroup runs both when route_align_fused() (small batches);
+// otherwise, given hist, the router writes each workgroup's per-expert counts (the align's
+// first pass, route_hist_ints(...) ints of hist) and align_place finishes, when that
+// chunk-count matrix is small (router.hip); else the router and launch_align.
 bool route_align_fused(int T, int E, int k, int n_loc);
+size_t route_hist_ints(int T, int E, int k, int n_loc);
 hipError_t launch_route_align(const float* logits, int T, int E, int k, int renorm, int e_lo, int n_loc,
                               int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
                               int32_t* sorted_tok, int32_t* pos, int32_t* hist, hipStream_t s);

@@ -48,12 +48,14 @@ __device__ __forceinline__ float group_sum(float x) {
 }
 
 // Route tokens wave, wave + nwaves, ... (TPW tokens per wave and step): softmax, top-k
-// by logit (ties to the lower id), weights over the picks or over all experts.  With
-// TO_LDS the ids are also stored to lds_ids[t*k + r] for an align in the same workgroup.
-template <int LPT, int VPL, int KMAX, bool TO_LDS>
+// by logit (ties to the lower id), weights over the picks or over all experts.  LDS_OUT
+// kLdsIds: the ids are also stored to lds[t*k + r] for an align in the same workgroup;
+// kLdsHist: each pick of a local expert (ids e_lo + [0, n_loc)) adds 1 to lds[id - e_lo].
+constexpr int kLdsNone = 0, kLdsIds = 1, kLdsHist = 2;
+template <int LPT, int VPL, int KMAX, int LDS_OUT>
 __device__ __forceinline__ void route_rows(const float* __restrict__ logits, int T, int E, int k, int renorm,
-                                           int32_t* __restrict__ ids, float* __restrict__ wts, int* lds_ids,
-                                           int wave, int nwaves) {
+                                           int32_t* __restrict__ ids, float* __restrict__ wts, int* lds,
+                                           int wave, int nwaves, int e_lo = 0, int n_loc = 0) {
   constexpr int TPW = 64 / LPT;
   constexpr int KPL = (KMAX + LPT - 1) / LPT;   // picks held per lane
   const int lane = threadIdx.x & 63;
@@ -132,7 +134,11 @@ __device__ __forceinline__ void route_rows(const float* __restrict__ logits, int
         const int r = j * LPT + li;
         if (r < k) {
           ids[static_cast<long long>(t) * k + r] = myi[j];
-          if constexpr (TO_LDS) lds_ids[t * k + r] = myi[j];
+          if constexpr (LDS_OUT == kLdsIds) lds[t * k + r] = myi[j];
+          if constexpr (LDS_OUT == kLdsHist) {
+            const int g = myi[j] - e_lo;
+            if (g >= 0 && g < n_loc) atomicAdd(&lds[g], 1);
+          }
           wts[static_cast<long long>(t) * k + r] = ex[j] / denom;
         }
       }

@@ -276,14 +276,18 @@ def test_fused_moe_refuses_mis_shaped_scales_and_shared_weights(dev):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("name,T", [("qwen3-30b-a3b-local32", 200), ("qwen3-30b-a3b-local32", 600),
-                                    ("qwen3-30b-a3b-local32", 3000), ("deepseek-v2-lite", 700),
-                                    ("mixtral-8x7b", 500), ("mixtral-8x7b", 2900)])
+@pytest.mark.parametrize("name,T", [("qwen3-30b-a3b-local32", 100), ("qwen3-30b-a3b-local32", 200),
+                                    ("qwen3-30b-a3b-local32", 600), ("qwen3-30b-a3b-local32", 3000),
+                                    ("deepseek-v2-lite", 600), ("deepseek-v2-lite", 700),
+                                    ("deepseek-v2-lite", 4500), ("mixtral-8x7b", 500), ("mixtral-8x7b", 2900)])
 def test_layer_routing_paths(dev, name, T):
     """Batch sizes that take each routing path of the fused layer: the one-workgroup router + align
-    (up to 2 routing steps), the router then the one-workgroup align, and the router then the
-    many-workgroup align (from 4096 routed pairs: several chunks, a ragged last one).  Ids
-    bit-exact, output against the oracle."""
+    (up to 2 routing steps: Qwen3 100 tokens); the router writing each workgroup's per-expert counts
+    then the many-workgroup align's placement, a chunk per router workgroup with a ragged last one
+    (chunk-count matrices up to 2048 cells: Qwen3 200 and 600 tokens, Mixtral 500 and 2900); and with
+    larger matrices the router then the one-workgroup align (below 4096 routed pairs: DeepSeek-V2-Lite
+    600 tokens) or the two-pass many-workgroup align (Qwen3 3000, DeepSeek-V2-Lite 700 and 4500).
+    Ids bit-exact, output against the oracle."""
     inp = make_inputs(SHAPES[name], T, device="cpu", hidden=128, inter=64)
     out, ids, w = _run(inp, dev)
     rid, rw = oracle.route_topk(inp.logits, inp.shape.top_k, inp.shape.renormalize)
