@@ -320,10 +320,15 @@ template <int LPT, int VPL, int KMAX>
 __global__ __launch_bounds__(kAlignThreads) void route_align_kernel(
     const float* __restrict__ logits, int T, int E, int k, int renorm, int e_lo, int n_loc, int32_t* __restrict__ ids,
     float* __restrict__ wts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ sorted_flat, int32_t* __restrict__ sorted_tok, int32_t* __restrict__ pos) {
+    int32_t* __restrict__ sorted_flat, int32_t* __restrict__ sorted_tok, int32_t* __restrict__ pos, int rank) {
   extern __shared__ int lds[];
   int* s_ids = lds + align_lds_ints(n_loc);   // [T*k] after the align's histogram
-  route_rows<LPT, VPL, KMAX, kLdsIds>(logits, T, E, k, renorm, ids, wts, s_ids, threadIdx.x >> 6, kAlignWaves);
+  if (rank) {   // then [T*E] logits and [T*k] picked values
+    float* s_lg = reinterpret_cast<float*>(s_ids + T * k);
+    route_rank(logits, T, E, k, renorm, ids, wts, s_ids, s_lg, s_lg + T * E);
+  } else {
+    route_rows<LPT, VPL, KMAX, kLdsIds>(logits, T, E, k, renorm, ids, wts, s_ids, threadIdx.x >> 6, kAlignWaves);
+  }
   __syncthreads();
   if (T * k <= 64) {   // a decode step's few ids: one wave sorts them without further barriers
     if (threadIdx.x < 64) align_tiny(s_ids, T * k, k, e_lo, n_loc, counts, offsets, sorted_flat, sorted_tok, pos, lds);
@@ -339,21 +344,30 @@ constexpr size_t kRouteAlignMaxLds = 64 * 1024;
 
 int router_lanes(int E) { return E <= 8 ? 8 : E <= 128 ? 16 : 32; }
 
-size_t route_align_lds_bytes(int T, int k, int n_loc) {
-  return (static_cast<size_t>(align_lds_ints(n_loc)) + static_cast<size_t>(T) * k) * sizeof(int);
+// A token or two over wider routers take the rank selection (route_rank): the k argmax rounds
+// of route_rows are a chain of dependent lane-group reductions (~0.44 us each at 128 experts),
+// while ranking costs T*E*E compares on the one workgroup's VALU.  Measured (one box, cache-cold
+// Qwen3-30B-A3B 32-expert share): 1 token 23.2 -> 21.5 us; with the rank path up to T*E = 4096,
+// 8 tokens 49.4 -> 55.9 us and 32 tokens 66.6 -> 97.5 us.
+bool route_by_rank(int T, int E) { return E >= 16 && static_cast<long long>(T) * E <= 256; }
+
+size_t route_align_lds_bytes(int T, int E, int k, int n_loc) {
+  const size_t extra = route_by_rank(T, E) ? static_cast<size_t>(T) * E + static_cast<size_t>(T) * k : 0;
+  return (static_cast<size_t>(align_lds_ints(n_loc)) + static_cast<size_t>(T) * k + extra) * sizeof(int);
 }
 
 template <int LPT, int VPL>
 hipError_t launch_route_align_lv(const float* logits, int T, int E, int k, int renorm, int e_lo, int n_loc,
                                  int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* sorted_flat,
                                  int32_t* sorted_tok, int32_t* pos, hipStream_t s) {
-  const size_t lds = route_align_lds_bytes(T, k, n_loc);
+  const size_t lds = route_align_lds_bytes(T, E, k, n_loc);
+  const int rank = route_by_rank(T, E) ? 1 : 0;
   if (k <= 8)
     hipLaunchKernelGGL((route_align_kernel<LPT, VPL, 8>), dim3(1), dim3(kAlignThreads), lds, s, logits, T, E, k,
-                       renorm, e_lo, n_loc, ids, w, counts, offsets, sorted_flat, sorted_tok, pos);
+                       renorm, e_lo, n_loc, ids, w, counts, offsets, sorted_flat, sorted_tok, pos, rank);
   else
     hipLaunchKernelGGL((route_align_kernel<LPT, VPL, 32>), dim3(1), dim3(kAlignThreads), lds, s, logits, T, E, k,
-                       renorm, e_lo, n_loc, ids, w, counts, offsets, sorted_flat, sorted_tok, pos);
+                       renorm, e_lo, n_loc, ids, w, counts, offsets, sorted_flat, sorted_tok, pos, rank);
   return hipGetLastError();
 }
 
@@ -367,7 +381,7 @@ size_t route_hist_ints(int T, int E, int k, int n_loc) {
 bool route_align_fused(int T, int E, int k, int n_loc) {
   const long long per_step = static_cast<long long>(kAlignWaves) * (64 / router_lanes(E));
   return T >= 1 && E <= 256 && (T + per_step - 1) / per_step <= kRouteAlignMaxSteps &&
-         route_align_lds_bytes(T, k, n_loc) <= kRouteAlignMaxLds;
+         route_align_lds_bytes(T, E, k, n_loc) <= kRouteAlignMaxLds;
 }
 
 hipError_t launch_route_align(const float* logits, int T, int E, int k, int renorm, int e_lo, int n_loc,

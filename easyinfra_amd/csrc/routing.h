@@ -146,6 +146,82 @@ __device__ __forceinline__ void route_rows(const float* __restrict__ logits, int
   }
 }
 
+// Top-k by rank for a few tokens, by the whole workgroup: value i of token t is pick r of
+// the token when exactly r values of its row beat it (a larger logit, or an equal one at a
+// lower id): the picks and their order of route_rows' k argmax rounds, with no dependent
+// rounds.  NaN logits neither beat nor are picked; slots past a row's non-NaN values keep
+// id 0x7fffffff and value -inf, as there.  The T*E logits are staged in s_lg, the picked
+// values in s_pv[T*k], the ids in lds_ids[T*k]; ids and weights (pick r in lane r % 16 of
+// its token's 16-lane group, as route_rows with 16-lane groups) are written out.
+__device__ __forceinline__ void route_rank(const float* __restrict__ logits, int T, int E, int k, int renorm,
+                                           int32_t* __restrict__ ids, float* __restrict__ wts, int* lds_ids,
+                                           float* s_lg, float* s_pv) {
+  const int tid = threadIdx.x;
+  const int nthr = blockDim.x;
+  const int V = T * E;
+  const float NEG_INF = -__builtin_inff();
+  for (int i = tid; i < V; i += nthr) s_lg[i] = logits[i];
+  for (int i = tid; i < T * k; i += nthr) {
+    lds_ids[i] = 0x7fffffff;
+    s_pv[i] = NEG_INF;
+  }
+  __syncthreads();
+  int G = 16;   // lanes per value (a power of two within a DPP row)
+  while (G > 1 && V * G > nthr) G >>= 1;
+  const int per_pass = nthr / G;
+  for (int base = 0; base < V; base += per_pass) {
+    const int v = base + tid / G;
+    const int li = tid % G;
+    int beats = 0;
+    float x = 0.f;
+    int t = 0, i = 0;
+    if (v < V) {
+      t = v / E;
+      i = v - t * E;
+      x = s_lg[v];
+      const float* row = s_lg + t * E;
+      for (int j = li; j < E; j += G) {
+        const float y = row[j];
+        beats += ((y > x) | ((y == x) & (j < i))) ? 1 : 0;
+      }
+    }
+    if (G >= 2) beats += dpp_i<0xB1>(beats);
+    if (G >= 4) beats += dpp_i<0x4E>(beats);
+    if (G >= 8) beats += dpp_i<0x141>(beats);
+    if (G >= 16) beats += dpp_i<0x140>(beats);
+    if (v < V && li == 0 && x == x && beats < k) {
+      lds_ids[t * k + beats] = i;
+      s_pv[t * k + beats] = x;
+    }
+  }
+  __syncthreads();
+  for (int t0 = 0; t0 < T; t0 += nthr / 16) {
+    const int t = t0 + tid / 16;
+    const int li = tid % 16;
+    const bool tv = t < T;
+    const float mx = tv ? s_pv[t * k] : 0.f;
+    const float ex0 = (tv && li < k) ? expf(s_pv[t * k + li] - mx) : 0.f;
+    const float ex1 = (tv && li + 16 < k) ? expf(s_pv[t * k + li + 16] - mx) : 0.f;
+    float part = ex0 + ex1;
+    if (!renorm) {
+      part = 0.f;
+      if (tv)
+        for (int e = li; e < E; e += 16) part += expf(s_lg[t * E + e] - mx);
+    }
+    const float denom = group_sum<16>(part);
+    if (tv) {
+      if (li < k) {
+        ids[static_cast<long long>(t) * k + li] = lds_ids[t * k + li];
+        wts[static_cast<long long>(t) * k + li] = ex0 / denom;
+      }
+      if (li + 16 < k) {
+        ids[static_cast<long long>(t) * k + li + 16] = lds_ids[t * k + li + 16];
+        wts[static_cast<long long>(t) * k + li + 16] = ex1 / denom;
+      }
+    }
+  }
+}
+
 constexpr int kAlignWaves = 16;
 constexpr int kAlignThreads = kAlignWaves * 64;
 constexpr int kAlignBatch = 8;

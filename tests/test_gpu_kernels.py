@@ -248,6 +248,32 @@ def test_route_align_bit_exact(dev, T, E, k, e_lo, n_loc, renorm):
     assert np.array_equal(cpu(got["sorted_tok"])[:A].numpy(), ref["sorted_tok"])
 
 
+# A token or two over 16+ experts (T*E <= 256) route by rank inside the route+align kernel: each
+# value's pick slot is the number of values beating it.  Same ids in the same order as the
+# router's k argmax rounds, on rows full of ties, +-inf and NaN (NaN never picked; slots past a
+# row's non-NaN values hold 0x7fffffff), and bit-identical weights up to 128 experts (the same
+# 16-lane summation); above, within the router tests' tolerance.
+@pytest.mark.parametrize("T,E,k,renorm", [(1, 128, 8, True), (2, 128, 8, False), (1, 128, 8, False),
+                                          (4, 64, 6, True), (16, 16, 4, False), (1, 256, 8, True),
+                                          (2, 32, 32, True), (8, 32, 4, True)])
+def test_route_align_rank_selection_matches_router(dev, T, E, k, renorm):
+    g = torch.Generator().manual_seed(T * 7 + E)
+    logits = torch.round(torch.randn(T, E, generator=g) * 2.0)   # a handful of distinct values per row
+    logits[1::3, ::7] = float("inf")
+    logits[2::3, 3::11] = -float("inf")
+    if T > 1:
+        logits[1, : E - 3] = float("nan")                         # fewer than k non-NaN values
+    ids, w, _ = ops.route_align(logits.to(dev), k, E, 0, renorm)
+    rid, rw = ops.router_topk(logits.to(dev), k, renorm)
+    assert torch.equal(cpu(ids), cpu(rid))
+    if E <= 128:
+        torch.testing.assert_close(cpu(w), cpu(rw), rtol=0, atol=0, equal_nan=True)
+    fin = torch.isfinite(logits).all(dim=1)
+    if bool(fin.any()):
+        oid, ow = oracle.route_topk(logits[fin], k, renorm)
+        assert torch.equal(cpu(ids)[fin], oid)
+
+
 def test_route_align_empty(dev):
     ids, w, got = ops.route_align(torch.empty(0, 8, device=dev), 2, 8)
     assert ids.shape == (0, 2) and cpu(got["offsets"]).tolist() == [0] * 9
