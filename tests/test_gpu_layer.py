@@ -297,6 +297,36 @@ def test_layer_routing_paths(dev, name, T):
     assert float((cpu(out) - ref).abs().max()) <= 2e-3 * max(1.0, float(ref.abs().max()))
 
 
+# Full-size property: a token's output depends only on its own row and logits (routing per token,
+# each GEMM row accumulated in the same K order whatever the other rows, the combine summing a
+# token's slots in slot order), so permuting the tokens of a real-shape layer permutes its output
+# bit for bit, in bf16 and in W8A8 (x quantised per token, h per routed row).  Per-expert row
+# counts are unchanged by the permutation, so the same tiles run.
+@pytest.mark.slow
+@pytest.mark.parametrize("name,T,w8a8", [("mixtral-8x7b", 8192, False), ("mixtral-8x7b", 8192, True),
+                                         ("deepseek-v2-lite", 4096, False), ("qwen3-30b-a3b-local32", 2048, False),
+                                         ("mixtral-8x7b", 64, True), ("qwen3-30b-a3b-local32", 32, False)])
+def test_layer_token_permutation_is_exact(dev, name, T, w8a8):
+    shape = SHAPES[name]
+    inp = make_inputs(shape, T, device=dev)
+    kw = {}
+    wgu, wd = inp.w_gate_up, inp.w_down
+    if w8a8:
+        wgu, sgu = ops.quantize_weights_fp8(wgu)
+        wd, sd = ops.quantize_weights_fp8(wd)
+        kw = dict(w_scales=(sgu, sd), w8a8=True)
+    perm = torch.randperm(T, generator=torch.Generator().manual_seed(T)).to(dev)
+
+    def run(x, lg):
+        return ops.fused_moe(x, lg, shape.top_k, wgu, wd, renormalize=shape.renormalize,
+                             shared_gate_up=inp.shared_gate_up, shared_down=inp.shared_down,
+                             expert_range=inp.expert_range, out_dtype=torch.float32, **kw)
+
+    base = run(inp.x, inp.logits)
+    permuted = run(inp.x[perm].contiguous(), inp.logits[perm].contiguous())
+    assert torch.equal(cpu(permuted), cpu(base)[cpu(perm)])
+
+
 # Every token routed to the same experts: a few long segments beside empty ones, on the prefill
 # tiles (up to 256x256 with its persistent walk) and on the decode kernels.  Ids bit-exact, output
 # against the oracle with h rounded to bf16 as the layer stores it.
