@@ -327,6 +327,29 @@ def test_layer_token_permutation_is_exact(dev, name, T, w8a8):
     assert torch.equal(cpu(permuted), cpu(base)[cpu(perm)])
 
 
+# Full-size sharding property: the layer over all experts equals the sum of the layers over disjoint
+# expert windows (one GPU's share each, tokens without a resident expert giving zero rows), fp32
+# outputs.  Not bit for bit: each window picks its own tiles and K split from its row counts, so the
+# partial sums round differently; within rel-L2 1e-6.
+@pytest.mark.slow
+@pytest.mark.parametrize("name,T,windows", [("mixtral-8x7b", 8192, ((0, 2), (2, 4), (4, 6), (6, 8))),
+                                            ("mixtral-8x7b", 64, ((0, 3), (3, 8))),
+                                            ("deepseek-v2-lite", 4096, ((0, 16), (16, 48), (48, 64)))])
+def test_layer_is_the_sum_of_its_expert_windows(dev, name, T, windows):
+    shape = SHAPES[name]
+    inp = make_inputs(shape, T, device=dev)
+    E = shape.n_experts
+
+    def run(lo, hi):
+        return ops.fused_moe(inp.x, inp.logits, shape.top_k, inp.w_gate_up[lo:hi].contiguous(),
+                             inp.w_down[lo:hi].contiguous(), renormalize=shape.renormalize,
+                             expert_range=(lo, hi), out_dtype=torch.float32)
+
+    full = cpu(run(0, E))
+    parts = sum(cpu(run(lo, hi)) for lo, hi in windows)
+    assert oracle.rel_l2(parts, full) <= 1e-6
+
+
 # Every token routed to the same experts: a few long segments beside empty ones, on the prefill
 # tiles (up to 256x256 with its persistent walk) and on the decode kernels.  Ids bit-exact, output
 # against the oracle with h rounded to bf16 as the layer stores it.
