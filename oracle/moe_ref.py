@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
-checker (or, in the bench, as the timed CPU baseline).  The product path
+reference results are compared with (or, in the bench, as the timed CPU
+baseline).  The product path
 (``easyinfra_amd``) never calls it; it fails loudly when its HIP library is
 missing.
 
