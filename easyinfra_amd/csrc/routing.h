@@ -180,6 +180,7 @@ __device__ __forceinline__ void route_rank(const float* __restrict__ logits, int
       i = v - t * E;
       x = s_lg[v];
       const float* row = s_lg + t * E;
+#pragma unroll 8   // LDS reads in flight together: the loop is otherwise a chain of read latencies
       for (int j = li; j < E; j += G) {
         const float y = row[j];
         beats += ((y > x) | ((y == x) & (j < i))) ? 1 : 0;
