@@ -17,7 +17,7 @@ Prints ONE JSON line.  Besides the contract fields it carries:
                 (HBM-bound) and the per-kernel breakdown
   suite         the other workloads, warm and cache-cold: tiny fp32, DeepSeek-V2-Lite
                 (zipf + uniform twin, and routed by the DeepSeek-V3 gate), the DeepSeek-V3
-                gate alone, the Qwen3 local share at 1..2048 tokens, fp8 W8A8 Mixtral
+                gate alone, the Qwen3 local share at 1..2048 tokens, fp8 Mixtral (W8A8 and W8A16)
 """
 from __future__ import annotations
 
@@ -61,7 +61,53 @@ def parse():
                     help="counter-collection driver: a 1 GiB device copy (known bytes, calibrates FETCH_SIZE/"
                          "WRITE_SIZE) followed by two fused prefill layers and two 64-token decode layers; prints "
                          "no JSON line")
+    ap.add_argument("--trace-summary", default=None, metavar="KERNEL_TRACE_CSV",
+                    help="summarise a rocprofv3 kernel trace (its *_kernel_trace.csv): per kernel, the launch "
+                         "count, the mean over all launches and over the last --trace-last launches; prints a "
+                         "markdown table, no JSON line, and touches no GPU")
+    ap.add_argument("--trace-last", type=int, default=20,
+                    help="launches per kernel in the steady-state mean of --trace-summary (the bench's --steps)")
     return ap.parse_args()
+
+
+def _kernel_short_name(name):
+    """A kernel's name without its parameter list (template arguments kept)."""
+    name = name[5:] if name.startswith("void ") else name
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0 and not name.startswith("(anonymous", i):
+            return name[:i]
+    return name
+
+
+def trace_summary(path, last):
+    """Per-kernel launch statistics of a rocprofv3 kernel trace, in dispatch order: the bench's
+    roofline kernel is launched 2 * (warmup + steps) times (layer calls, then stage calls), and its
+    HIP-event mean covers the last `steps` of them, which the last-N column reproduces."""
+    import csv
+    by = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            by.setdefault(r["Kernel_Name"], []).append((int(r["Dispatch_Id"]), d))
+    rows = []
+    total = sum(d for v in by.values() for _, d in v)
+    for name, v in by.items():
+        v.sort()
+        ds = [d for _, d in v]
+        tail = ds[-last:]
+        rows.append((sum(ds), name, len(ds), sum(ds) / len(ds) / 1e3, sum(tail) / len(tail) / 1e3, len(tail)))
+    rows.sort(reverse=True)
+    print(f"| kernel | calls | mean, all calls (us) | mean, last N calls (us) | N | share |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for tot, name, n, avg, avg_tail, nt in rows:
+        short = _kernel_short_name(name)
+        short = short if len(short) <= 100 else short[:97] + "..."
+        print(f"| `{short}` | {n} | {avg:.1f} | {avg_tail:.1f} | {nt} | {100.0 * tot / total:.2f}% |")
 
 
 def timed(fn, steps, warmup, torch):
@@ -79,12 +125,15 @@ def timed(fn, steps, warmup, torch):
 
 
 def stage_times(inp, steps, warmup, torch, ops):
-    """Same kernels as the fused entry point, launched one by one with HIP events
-    between them on the launch stream; returns mean ms per stage."""
+    """Same kernels as the fused entry point (same tiles, the layer's K split of the down
+    projection, fp32 partial planes), launched one by one with HIP events between them on the
+    launch stream; returns mean ms per stage and the down projection's K split."""
     s = inp.shape
     T, H = inp.x.shape
     n_local = inp.w_gate_up.shape[0]
     A = T * s.top_k
+    ks = ops.fused_moe_down_split(T, H, s.inter, s.n_experts, s.top_k, n_local, 0, inp.x.dtype,
+                                  1 if s.renormalize else 0)
     names = ["router", "align", "gate_up_silu", "down", "combine"]
     sums = [0.0] * len(names)
 
@@ -96,7 +145,7 @@ def stage_times(inp, steps, warmup, torch, ops):
         evs[2].record()
         h = ops.gemm_gate_up_silu(inp.x, inp.w_gate_up, al["offsets"], A, a_rows=al["sorted_tok"])
         evs[3].record()
-        y = ops.gemm_down(h, inp.w_down, al["offsets"], A, out_dtype=torch.bfloat16)
+        y = ops.gemm_down(h, inp.w_down, al["offsets"], A, out_dtype=torch.float32, k_split=ks)
         evs[4].record()
         ops.combine(y, al["pos"], w, out_dtype=torch.bfloat16)
         evs[5].record()
@@ -110,7 +159,7 @@ def stage_times(inp, steps, warmup, torch, ops):
         torch.cuda.synchronize()
         for i in range(len(names)):
             sums[i] += evs[i].elapsed_time(evs[i + 1])
-    return {n: v / steps for n, v in zip(names, sums)}
+    return {n: v / steps for n, v in zip(names, sums)}, ks
 
 
 def cpu_baseline(inp, n_tokens, runs, torch):
@@ -146,16 +195,20 @@ def cpu_baseline(inp, n_tokens, runs, torch):
 
 
 def traffic_from_profiles(kernel_tag):
-    """HBM bytes per launch of one kernel, from counter runs of ``--traffic-run``
-    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for the 1 GiB copy)."""
+    """HBM bytes per launch of one kernel, from counter runs of ``--traffic-run`` (FETCH_SIZE and
+    WRITE_SIZE, each scaled by what it reads for the 1 GiB copy), as recorded in
+    profiles/traffic.json; returns (bytes, a note naming that file and its run), or (None, None)."""
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
-        return None
+        return None, None
     try:
-        rec = json.loads(f.read_text()).get(kernel_tag)
-        return None if rec is None else int(rec["traffic_bytes"])
-    except (ValueError, OSError, KeyError, TypeError):
-        return None
+        data = json.loads(f.read_text())
+        rec = data.get(kernel_tag)
+        if rec is None:
+            return None, None
+        return int(rec["traffic_bytes"]), f"profiles/traffic.json ({data.get('_run', 'counter run')})"
+    except (ValueError, OSError, KeyError, TypeError, AttributeError):
+        return None, None
 
 
 def traffic_run(torch, ops, shape, make_inputs, tokens):
@@ -326,6 +379,9 @@ def suite(torch, ops, mix_inp, steps, warmup):
                                                                      mix_inp.w_gate_up, mix_inp.w_down)
         out.append(layer_case(f"mixtral-8x7b fp8-e4m3 W8A8 T={T}", sub, torch, ops, steps, warmup, flush, w8a8=True,
                               fp8w=(qgu, qd, (sgu, sd))))
+        # W8A16 (e4m3 weights widened to bf16, bf16 MFMA): the fp8 mode within 5e-2 rel-L2 of the bf16 layer
+        out.append(layer_case(f"mixtral-8x7b fp8-e4m3 W8A16 T={T}", sub, torch, ops, steps, warmup, flush,
+                              fp8w=(qgu, qd, (sgu, sd))))
     return out
 
 
@@ -375,6 +431,9 @@ def profile_case(torch, ops, spec):
 
 def main():
     args = parse()
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.trace_last)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the MoE expert path is built and measured on a single "
               "MI355X (multi-GPU expert parallelism is out of scope); run with --gpus 1", file=sys.stderr)
@@ -406,14 +465,19 @@ def main():
     ms = timed(layer, args.steps, args.warmup, torch)
     A = T * k
     flops = layer_flops(A, T, H, I)
-    stages = stage_times(inp, args.steps, args.warmup, torch, ops)
+    stages, down_split = stage_times(inp, args.steps, args.warmup, torch, ops)
     gu_flops = 4.0 * A * H * I
     gu_ms = stages["gate_up_silu"]
     achieved = gu_flops / (gu_ms * 1e-3) / 1e12
+    traffic, traffic_src = traffic_from_profiles("gate_up_silu_prefill")
     roof = {"bound": "mfma", "kernel": "grouped_gemm_pp3p_kernel<2,8,false> (256x256 bf16 gate/up + SiLU*mul, persistent)",
             "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic_from_profiles("gate_up_silu_prefill"),
-            "flops_per_launch": gu_flops, "mean_launch_ms": round(gu_ms, 4)}
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
+            "flops_per_launch": gu_flops, "mean_launch_ms": round(gu_ms, 4),
+            "launches_averaged": args.steps,
+            "launches_note": f"the last {args.steps} of {2 * (args.warmup + args.steps)} launches of this kernel in the "
+                             f"run: the layer's {args.warmup} + {args.steps} calls, then {args.warmup} warm-up and "
+                             f"{args.steps} timed stage calls (HIP events on the launch stream)"}
 
     # decode batch (HBM-bound): the first decode-tokens rows of the same layer
     Td = args.decode_tokens
@@ -450,6 +514,7 @@ def main():
         "cpu_baseline": cpu,
         "decode": decode,
         "kernels_ms": {k_: round(v, 4) for k_, v in stages.items()},
+        "down_k_split": down_split,
         "suite": cases,
     }
     print(json.dumps(line), flush=True)

@@ -26,6 +26,7 @@ _f32p = POINTER(ctypes.c_float)
 SIGNATURES = {
     "eimoe_abi_version": (c_int, []),
     "eimoe_last_error": (c_char_p, []),
+    "eimoe_release_streams": (c_int, []),
     "eimoe_router_topk": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "eimoe_router_grouped_topk": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int, c_float,
                                           c_void_p, c_void_p, c_void_p]),
@@ -57,6 +58,7 @@ SIGNATURES = {
                               c_void_p, c_int, c_void_p, c_int, c_void_p]),
     "eimoe_quantize_rows_fp8": (c_int, [c_void_p, c_int, c_longlong, c_int, c_void_p, c_void_p, c_void_p]),
     "eimoe_fused_moe_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "eimoe_fused_moe_down_split": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "eimoe_fused_moe": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int,
                                 c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int,
                                 c_void_p, c_size_t, c_void_p, c_void_p, c_void_p]),

@@ -39,7 +39,8 @@ int hip_check(hipError_t e, const char* what) {
 inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
 
 // A second stream per (host thread, device) with its fork/join events, created on first
-// use and kept until the process ends: the fused layer runs the shared experts on it so
+// use and kept until eimoe_release_streams() on that thread (or the process's end): the fused
+// layer runs the shared experts on it so
 // their launches overlap the routed ones (each alone ends in a mostly idle CU round).
 // Default priority, non-blocking; the fork/join through events also holds under graph
 // capture of the caller's stream.
@@ -49,10 +50,12 @@ struct AuxStream {
 };
 constexpr int kMaxDevices = 64;
 
+thread_local AuxStream g_aux[kMaxDevices];
+
 // *out stays null when the stream does not exist yet and may not be created now (the
 // caller's stream is capturing: creating a stream then would invalidate the capture).
 hipError_t aux_stream(AuxStream** out, bool may_create) {
-  thread_local AuxStream aux[kMaxDevices];
+  AuxStream* aux = g_aux;
   *out = nullptr;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -173,8 +176,12 @@ FusedLayout fused_layout(int T, int H, int I, int E, int k, int n_local, int Is,
   const size_t A = static_cast<size_t>(T) * k;
   L.rows_hint = local_rows_hint(T, k, E, n_local);
   L.h_terms = (flags & EIMOE_H_SPLIT) ? 2 : 1;
-  L.y_dtype =
-      ((flags & (EIMOE_Y_F32 | EIMOE_H_SPLIT | EIMOE_FP32)) || out_dtype == EIMOE_F32) ? EIMOE_F32 : EIMOE_BF16;
+  // The per-assignment outputs stay in fp32 whatever the output type: the combine sums a token's
+  // slots (and split-K planes) in fp32 and rounds once.  With bf16 planes each partial sum was
+  // rounded before the combine, which put the 8192-token Mixtral-8x7B layer's bf16 output 5.8e-2
+  // from the fp32 oracle against 2.0e-2 + half an ulp for a single rounding.
+  (void)out_dtype;
+  L.y_dtype = EIMOE_F32;
   const size_t hb = (flags & EIMOE_FP32) ? 4 : 2;   // bytes per h element
   L.k_split = pick_down_split(static_cast<int>(A), L.rows_hint, n_local, H, I,
                               static_cast<int>(elem_size(L.y_dtype)), (flags & EIMOE_W8A8) != 0);
@@ -287,6 +294,28 @@ int run_down(const void* h, int I, const void* w, int w_dtype, const float* w_sc
 extern "C" {
 
 int eimoe_abi_version(void) { return EIMOE_ABI_VERSION; }
+
+int eimoe_release_streams(void) {
+  int prev = 0;
+  int rc = hip_check(hipGetDevice(&prev), "current device");
+  if (rc) return rc;
+  for (int dev = 0; dev < kMaxDevices; ++dev) {
+    AuxStream& a = g_aux[dev];
+    if (!a.stream && !a.fork && !a.join) continue;
+    int r = hip_check(hipSetDevice(dev), "set device");
+    // the stream's work (shared experts of a layer still running) ends before it is destroyed
+    if (!r && a.stream) r = hip_check(hipStreamSynchronize(a.stream), "aux stream synchronize");
+    if (!r && a.stream) r = hip_check(hipStreamDestroy(a.stream), "aux stream destroy");
+    if (!r && a.fork) r = hip_check(hipEventDestroy(a.fork), "fork event destroy");
+    if (!r && a.join) r = hip_check(hipEventDestroy(a.join), "join event destroy");
+    if (r) {
+      hipSetDevice(prev);
+      return r;
+    }
+    a = AuxStream{};
+  }
+  return hip_check(hipSetDevice(prev), "restore device");
+}
 
 const char* eimoe_last_error(void) { return g_err; }
 
@@ -677,6 +706,12 @@ size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_
   (void)E;
   if (T < 0 || H < 1 || I < 1 || k < 1 || n_local < 1 || shared_inter < 0) return 0;
   return fused_layout(T, H, I, E, k, n_local, shared_inter, out_dtype, flags).total;
+}
+
+int eimoe_fused_moe_down_split(int T, int H, int I, int E, int k, int n_local, int shared_inter, int out_dtype,
+                               int flags) {
+  if (T < 0 || H < 1 || I < 1 || k < 1 || n_local < 1 || shared_inter < 0) return 0;
+  return fused_layout(T, H, I, E, k, n_local, shared_inter, out_dtype, flags).k_split;
 }
 
 }  // extern "C"

@@ -1393,9 +1393,13 @@ hipError_t launch_grouped_gemm_f32(const GemmArgs& p, int epi, int max_rows, int
     const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) /
                        (p.S > 0 ? p.S : 1);
     tile = avg >= 32 ? kTileM : avg >= 12 ? kTileS : kTileXS;
-    while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) ++tile;
   }
+  // No 256x256 or streaming fp32 kernel: those requests take the 128x128 tile.  Whatever the
+  // start, step down until the tile's output columns divide N (the tile's columns are its grid's
+  // only bound on N), and refuse a tile that still does not fit rather than leave columns unwritten.
   if (tile == kTileL || tile == kTileStream) tile = kTileM;
+  while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) ++tile;
+  if (p.N % gemm_out_cols_per_tile(tile, epi) != 0) return hipErrorInvalidValue;
   return epi == kEpiSiluF32 ? launch_epi_f32<kEpiSiluF32>(p, max_rows, tile, s)
                             : launch_epi_f32<kEpiStoreF32>(p, max_rows, tile, s);
 }

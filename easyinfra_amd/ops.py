@@ -392,9 +392,20 @@ def quantize_weights_fp8(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     return quantize_rows_fp8(w)
 
 
+def release_streams() -> None:
+    """Release this thread's second stream (shared experts) and its events; the next fused_moe call
+    with shared experts creates them again."""
+    call("eimoe_release_streams")
+
+
 def fused_moe_workspace_bytes(T, H, I, E, k, n_local, shared_inter=0, out_dtype=torch.bfloat16, flags=0) -> int:
     return int(_lib.lib().eimoe_fused_moe_workspace_bytes(T, H, I, E, k, n_local, shared_inter,
                                                            _DT[out_dtype], flags))
+
+
+def fused_moe_down_split(T, H, I, E, k, n_local, shared_inter=0, out_dtype=torch.bfloat16, flags=0) -> int:
+    """The down projection's K split fused_moe picks for this layer (its fp32 partial planes)."""
+    return int(_lib.lib().eimoe_fused_moe_down_split(T, H, I, E, k, n_local, shared_inter, _DT[out_dtype], flags))
 
 
 def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: int, w_gate_up: torch.Tensor,
@@ -422,6 +433,8 @@ def fused_moe(hidden_states: torch.Tensor, router_logits: torch.Tensor, top_k: i
     fp32 hidden states with fp32 weights run the fp32 layer (fp32 MFMA, fp32 h and y: the
     reference's fp32 F.linear path, native_moe.py:56-103); fp32 hidden states with bf16 or fp8
     weights are refused rather than rounded.
+    The per-assignment expert outputs are kept in fp32 and summed by the combine in fp32 with one
+    rounding to ``out_dtype`` (``y_fp32`` is accepted for compatibility and has no effect).
     ``h_split=True`` is the precise mode: h = silu(g)*u is kept as a pair of bf16 terms (hi + lo)
     and the down projection runs once per term, so h carries ~16 significant bits instead of 8
     (twice the down projection's time; per-assignment outputs in fp32).

@@ -38,6 +38,13 @@ def _period(b_list: List[torch.Tensor]) -> int:
     return n
 
 
+def _to_device(values, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """A small host list on the device without blocking the host: staged in pinned memory and
+    copied on the current stream (the caching host allocator keeps the staging block until the
+    copy has run)."""
+    return torch.tensor(values, dtype=dtype, pin_memory=True).to(device, non_blocking=True)
+
+
 def _ptr_table(b_list: List[torch.Tensor], device: torch.device) -> torch.Tensor:
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            tuple(b.data_ptr() for b in b_list))
@@ -45,8 +52,11 @@ def _ptr_table(b_list: List[torch.Tensor], device: torch.device) -> torch.Tensor
     if t is None:
         if len(_PTR_TABLES) >= _MAX_TABLES:
             _PTR_TABLES.pop(next(iter(_PTR_TABLES)))
-        t = torch.tensor(key[1], dtype=torch.int64).to(device)
+        t = _to_device(list(key[1]), torch.int64, device)
         _PTR_TABLES[key] = t
+    # A cached table may be read on a stream other than the one it was made on: mark every use, so
+    # that once evicted its memory is not handed out again before the kernels reading it have run.
+    t.record_stream(torch.cuda.current_stream(device))
     return t
 
 
@@ -69,9 +79,10 @@ def hip_grouped_gemm_single(A: torch.Tensor, B_list: List[torch.Tensor], block_s
         raise ValueError(f"A has {A.shape[1]} columns, the weights K={K}")
     p = _period(B_list)
     table = _ptr_table(B_list[:p], A.device)
-    off = torch.zeros(len(block_sizes) + 1, dtype=torch.int32)
-    off[1:] = torch.cumsum(torch.tensor(block_sizes, dtype=torch.int64), 0).to(torch.int32)
-    off = off.to(A.device)
+    bounds = [0]
+    for b in block_sizes:
+        bounds.append(bounds[-1] + int(b))
+    off = _to_device(bounds, torch.int32, A.device)
     c = torch.empty(M, N, dtype=A.dtype, device=A.device)
     call("eimoe_grouped_gemm_ptrs", A.data_ptr(), None, A.shape[0], A.stride(0), table.data_ptr(), p, N, K,
          off.data_ptr(), len(block_sizes), p, M, c.data_ptr(), _lib.BF16, 0, ops._stream(A))

@@ -44,7 +44,8 @@ enum { EIMOE_F32 = 0, EIMOE_BF16 = 1, EIMOE_FP8 = 2 };
 /* flags for eimoe_fused_moe */
 enum {
   EIMOE_RENORMALIZE = 1, /* renormalise the top-k weights (norm_topk_prob) */
-  EIMOE_Y_F32 = 2,       /* keep the per-assignment expert outputs in fp32 (default: output dtype) */
+  EIMOE_Y_F32 = 2,       /* accepted for compatibility, no effect: the per-assignment expert outputs
+                            are always kept in fp32 and the combine rounds once to the output type */
   EIMOE_W8A8 = 4,        /* fp8 weights: also quantise activations per token and run the fp8 MFMA */
   EIMOE_ROUTING_IN = 8,  /* topk_ids / topk_w are inputs (routing done by the caller, e.g. with
                             eimoe_router_grouped_topk); logits are not read and may be NULL */
@@ -70,6 +71,14 @@ enum { EIMOE_TILE_AUTO = 0, EIMOE_TILE_256x256 = 1, EIMOE_TILE_128x128 = 2, EIMO
 
 int eimoe_abi_version(void);
 const char* eimoe_last_error(void);
+
+/* Releases the calling thread's second stream and its two events (one set per device, created by
+ * the first eimoe_fused_moe call with shared experts on that thread and device), after waiting for
+ * the work queued on them.  No counterpart in the reference (its shared experts run on the caller's
+ * stream, moe_all2all.py:535-537); for callers that end worker threads or want the stream back
+ * before the process ends.  A later eimoe_fused_moe call creates them again.  Restores the current
+ * device. */
+int eimoe_release_streams(void);
 
 /* Router: softmax -> top-k -> optional renormalisation.
  * Replaces Qwen3MoeSparseMoeBlock._routing (models/qwen3_moe/modeling_qwen3_moe.py:255-266).
@@ -231,6 +240,14 @@ int eimoe_moe_prologue(const void* hidden, const void* residual, const void* nor
 size_t eimoe_fused_moe_workspace_bytes(int T, int H, int I, int E, int k, int n_local, int shared_inter,
                                        int out_dtype, int flags);
 
+/* The K split of the down projection that eimoe_fused_moe picks for these arguments: its
+ * per-assignment outputs are that many fp32 planes [T*k, H], summed by the combine.  No counterpart
+ * in the reference (its down projection is one unsplit launch, fused_moe.py:463-476); for callers
+ * that time the layer's stages through the op-level entry points and want the same launches.
+ * Returns 0 for arguments eimoe_fused_moe_workspace_bytes refuses. */
+int eimoe_fused_moe_down_split(int T, int H, int I, int E, int k, int n_local, int shared_inter, int out_dtype,
+                               int flags);
+
 /* The whole layer: hidden_states, router logits and top_k in, combined output out.
  * Composes router -> align -> gate/up+SiLU (gathering x rows directly) -> down -> combine
  * (+ shared experts), i.e. MoeAll2AllBlock's stages at ep=1 (blocks/moe/moe_all2all.py:85-95)
@@ -253,7 +270,8 @@ int eimoe_fused_moe(const void* x, const float* logits, int T, int H, int I, int
  * counterpart in the reference.  Same arguments and results as eimoe_fused_moe; its scratch is a
  * static device array of eimoe_fused_moe_static_bytes() (64 MiB) that each GPU holds from the
  * first call until the process ends, so it fits decode-sized layers (a Mixtral-8x7B layer up to
- * ~1k tokens; eimoe_fused_moe_workspace_bytes gives the need) and returns EIMOE_ERR_WORKSPACE,
+ * 545 tokens with either output type; eimoe_fused_moe_workspace_bytes gives the need) and returns
+ * EIMOE_ERR_WORKSPACE,
  * launching nothing, when a layer needs more.  It calls no hipMalloc/hipFree and creates no
  * stream or event (shared experts run on `stream` after the routed ones).  Every call on a GPU
  * uses that GPU's one scratch array: calls that overlap on one GPU (other streams, other host

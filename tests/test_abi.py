@@ -171,9 +171,32 @@ def test_fused_validation_and_workspace():
     ws = _lib.lib().eimoe_fused_moe_workspace_bytes(16, 256, 128, 8, 2, 8, 0, _lib.BF16, 1)
     ws_sh = _lib.lib().eimoe_fused_moe_workspace_bytes(16, 256, 128, 8, 2, 8, 256, _lib.BF16, 1)
     ws_f32 = _lib.lib().eimoe_fused_moe_workspace_bytes(16, 256, 128, 8, 2, 8, 0, _lib.F32, 1)
-    assert 0 < ws < ws_sh and ws < ws_f32
-    # h (A*I bf16) and y (A*H) dominate: at least that much
-    assert ws >= 32 * 128 * 2 + 32 * 256 * 2
+    # the per-assignment outputs y are fp32 whatever the output type
+    assert 0 < ws < ws_sh and ws == ws_f32
+    # h (A*I bf16) and y (A*H fp32) dominate: at least that much
+    assert ws >= 32 * 128 * 2 + 32 * 256 * 4
+
+
+def test_fused_down_split_query():
+    """eimoe_fused_moe_down_split: the layer's own choice (a power of two dividing the K steps), 0
+    where the workspace query refuses the arguments."""
+    L = _lib.lib()
+    for T, H, I, E, k, n in [(8192, 4096, 14336, 8, 2, 8), (64, 4096, 14336, 8, 2, 8), (2048, 2048, 768, 128, 8, 32),
+                             (4096, 2048, 1408, 64, 6, 64), (1, 256, 128, 8, 2, 8)]:
+        ks = L.eimoe_fused_moe_down_split(T, H, I, E, k, n, 0, _lib.BF16, 1)
+        assert ks in (1, 2, 4, 8) and I % (64 * ks) == 0
+    assert L.eimoe_fused_moe_down_split(16, 256, 128, 8, 0, 8, 0, _lib.BF16, 1) == 0
+
+
+def test_static_scratch_limit_matches_the_documented_token_count():
+    """The header and INTEGRATION.md give the largest Mixtral-8x7B layer (H 4096, I 14336, 8 experts,
+    top-2) the 64 MiB static scratch holds: 545 tokens with bf16 or fp32 output."""
+    L = _lib.lib()
+    cap = L.eimoe_fused_moe_static_bytes()
+    assert cap == 64 << 20
+    for odt in (_lib.BF16, _lib.F32):
+        need = lambda T: L.eimoe_fused_moe_workspace_bytes(T, 4096, 14336, 8, 2, 8, 0, odt, 1)
+        assert need(545) <= cap < need(546)
 
 
 def test_ops_refuse_cpu_tensors():

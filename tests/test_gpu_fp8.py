@@ -127,10 +127,13 @@ def test_fp8_mixtral_real_shape(dev, T):
         out = cpu(ops.fused_moe(inp.x, inp.logits, 2, qgu, qd, w_scales=(sgu, sd), out_dtype=torch.float32,
                                 w8a8=(mode == "w8a8")))
         own = oracle.moe_forward_fp8(x, lg, 2, cpu(qgu), cpu(sgu), cpu(qd), cpu(sd), True, mode=mode)
-        res[mode] = (oracle.rel_l2(out, ref), oracle.rel_l2(out, own))
+        # the bf16 output, as the benchmark times it
+        out16 = cpu(ops.fused_moe(inp.x, inp.logits, 2, qgu, qd, w_scales=(sgu, sd), w8a8=(mode == "w8a8"))).float()
+        res[mode] = (oracle.rel_l2(out, ref), oracle.rel_l2(out, own), oracle.rel_l2(out16, ref))
         print("PARITY " + json.dumps({"case": f"mixtral-8x7b-fp8 {mode} T={T}", "rows": T,
-                                      "rel_l2_vs_bf16_ref": res[mode][0], "rel_l2_vs_fp8_oracle": res[mode][1]},
+                                      "rel_l2_vs_bf16_ref": res[mode][0], "rel_l2_vs_fp8_oracle": res[mode][1],
+                                      "bf16_out_rel_l2_vs_bf16_ref": res[mode][2]},
                                      sort_keys=True), flush=True)
     assert res["w8a16"][1] <= 1e-2 and res["w8a8"][1] <= 1e-2
-    assert res["w8a16"][0] <= 5e-2
-    assert res["w8a8"][0] <= 7.5e-2
+    assert res["w8a16"][0] <= 5e-2 and res["w8a16"][2] <= 5e-2
+    assert res["w8a8"][0] <= 7.5e-2 and res["w8a8"][2] <= 7.5e-2

@@ -428,6 +428,70 @@ def test_persistent_gemm_bit_exact_with_one_tile_kernel(dev, w8a8, n_seg):
         assert torch.equal(cpu(dn(off_t, ks)), cpu(dn(off_pad_t, ks)))
 
 
+def _carve_above_bit31(dev, tensors):
+    """Copies of `tensors` inside one device allocation, at addresses with bit 31 set and no 4 GiB
+    boundary inside the block: a slice of a plain allocation a little over 2 GiB always holds such a
+    window.  Returns (the allocation, the copies)."""
+    sizes = [(t.numel() * t.element_size() + 255) // 256 * 256 for t in tensors]
+    need = sum(sizes)
+    big = torch.empty(2 ** 31 + 2 * need + 512, dtype=torch.uint8, device=dev)
+    base = big.data_ptr()
+    c = (base + 255) // 256 * 256
+    while not ((c >> 31) & 1 and (c % 2 ** 32) + need <= 2 ** 32):
+        c = (c | (2 ** 31 - 1)) + 1 if not (c >> 31) & 1 else (c | (2 ** 32 - 1)) + 1 + 2 ** 31
+    assert c + need <= base + big.numel()
+    out, o = [], c - base
+    for t, n in zip(tensors, sizes):
+        v = big[o:o + t.numel() * t.element_size()].view(t.dtype).view(t.shape)
+        v.copy_(t)
+        assert (v.data_ptr() >> 31) & 1
+        out.append(v)
+        o += n
+    return big, out
+
+
+# Operands whose base address has bit 31 set, on the persistent 256x256 kernel: it takes its buffer
+# bases from the first lane as two 32-bit halves, and a sign-extended low half would turn such a
+# base into 0xffffffff........  The same GEMMs on ordinary buffers must match bit for bit.
+@pytest.mark.parametrize("w8a8", [False, True])
+def test_persistent_gemm_operands_with_address_bit31(dev, w8a8):
+    g = torch.Generator().manual_seed(41 + w8a8)
+    H, I, T = 512, 512, 600
+    counts = [300, 1, 513, 129, 64]
+    E = len(counts)
+    off, off_t = _segments(counts)
+    off_t = off_t.to(dev)
+    rows = int(off[-1])
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32).to(dev)
+    w_gu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    w_d = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    hs = torch.randn(rows, I, generator=g).to(torch.bfloat16).to(dev)
+    if w8a8:
+        xq, sx = ops.quantize_rows_fp8(x)
+        qgu, sgu = ops.quantize_weights_fp8(w_gu)
+        qd, sd = ops.quantize_weights_fp8(w_d)
+        hq, sh = ops.quantize_rows_fp8(hs)
+        operands = [xq, sx, a_rows, qgu, sgu, hq, sh, qd, sd]
+
+        def run(xq, sx, a_rows, qgu, sgu, hq, sh, qd, sd):
+            return (ops.gemm_gate_up_silu_w8a8(xq, sx, qgu, sgu, off_t, rows, a_rows=a_rows, tile=1),
+                    ops.gemm_down_w8a8(hq, sh, qd, sd, off_t, rows, k_split=2, tile=1))
+    else:
+        operands = [x, a_rows, w_gu, hs, w_d]
+
+        def run(x, a_rows, w_gu, hs, w_d):
+            return (ops.gemm_gate_up_silu(x, w_gu, off_t, rows, a_rows=a_rows, tile=1),
+                    ops.gemm_down(hs, w_d, off_t, rows, out_dtype=torch.float32, k_split=2, tile=1))
+    want = [cpu(t) for t in run(*operands)]
+    big, high = _carve_above_bit31(dev, operands)
+    got = [cpu(t) for t in run(*high)]
+    torch.cuda.synchronize()
+    del big, high
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+
+
 # The weight-streaming kernel (tile 5) picks its column width (8/4/2 fragments), its K split
 # over waves and its register ring depth (2 or 1) from the shapes, or, for grids this small,
 # the short-stream mode (K split over 4 or 8 waves, at most 4 k-steps each, all in flight:
@@ -625,3 +689,34 @@ def test_fp32_gemms(dev, tile, k_split):
         href = gu[:, :I] * torch.sigmoid(gu[:, :I]) * gu[:, I:]
         torch.testing.assert_close(h[a:b], href, rtol=2e-5, atol=2e-6)
         torch.testing.assert_close(y[a:b], h[a:b] @ wd[e].double().T, rtol=2e-5, atol=2e-6)
+
+
+# The streaming tile has no fp32 kernel: an explicit request runs on the LDS tiles, stepping down
+# until the tile's output columns divide N.  Its host check admits any multiple of its own 16 SiLU
+# / 32 output columns, so gate/up with I = 96 (not a multiple of the 128x128 tile's 64 SiLU
+# columns) and the down / grouped GEMM with N = 192 (not a multiple of 128) must still write every
+# column.
+@pytest.mark.parametrize("tile", [5])
+def test_fp32_gemms_explicit_tile_narrow_columns(dev, tile):
+    counts = [40, 3, 77]
+    g = torch.Generator().manual_seed(31 + tile)
+    H, I, Id = 192, 96, 128
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    x = torch.randn(rows, H, generator=g)
+    wgu = torch.randn(E, 2 * I, H, generator=g) * 0.05
+    hd = torch.randn(rows, Id, generator=g)
+    wd = torch.randn(E, H, Id, generator=g) * 0.05
+    h = cpu(ops.gemm_gate_up_silu(x.to(dev), wgu.to(dev), off_t.to(dev), rows, tile=tile)).double()
+    y = cpu(ops.gemm_down(hd.to(dev), wd.to(dev), off_t.to(dev), rows, out_dtype=torch.float32,
+                          tile=tile)).sum(0).double()
+    c = cpu(ops.grouped_gemm(hd.to(dev), wd.to(dev), off_t.to(dev), rows, out_dtype=torch.float32, tile=tile)).double()
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        gu = x[a:b].double() @ wgu[e].double().T
+        href = gu[:, :I] * torch.sigmoid(gu[:, :I]) * gu[:, I:]
+        torch.testing.assert_close(h[a:b], href, rtol=2e-5, atol=2e-6)
+        yref = hd[a:b].double() @ wd[e].double().T
+        torch.testing.assert_close(y[a:b], yref, rtol=2e-5, atol=2e-6)
+        torch.testing.assert_close(c[a:b], yref, rtol=2e-5, atol=2e-6)
