@@ -456,10 +456,17 @@ __device__ __forceinline__ void pin_issue() {
 // A's 1 KiB blocks (8 rows each) are interleaved over the NW waves, block i * NW + wave, so the
 // first A_CNT of them per wave cover the first 8 * NW * A_CNT rows: a short tile loads only its
 // rows.  B's blocks are contiguous per wave.
+// b_nt (uniform): the weight loads carry the non-temporal hint.  When every weight panel is read by
+// one m-tile only (decode batches: a segment's rows fit one tile), streaming them past the caches
+// measured 13-20 % faster (Mixtral-8x7B 64 tokens, cold: bf16 down 176 -> 142 us on 128x128 tiles,
+// W8A8 gate/up 186 -> 167 us and down 82.5 -> 74.6 us on 32x128; a plain 1 KiB-per-instruction HBM
+// read 6.0-6.3 -> 6.7-7.0 TB/s); where a panel serves several m-tiles it costs the L2 reuse (W8A8
+// 256-token down on 32x128 tiles 150 -> 195 us), so the launcher sets it only for one m-tile per
+// segment.
 template <int A_CNT, int B_PW, int NW, int A_PW>
 __device__ __forceinline__ void issue_slab_dma(const BufRef& a, const BufRef& b, const uint32_t (&a_voff)[A_PW],
                                                const uint32_t (&b_voff)[B_PW], uint16_t* sA, uint16_t* sB, int wave,
-                                               int soff) {
+                                               int soff, bool b_nt) {
 #if defined(__HIP_DEVICE_COMPILE__)  // device-only builtins; the host pass only needs the declaration
   const auto rA = make_rsrc(a.base, a.bytes);
   const auto rB = make_rsrc(b.base, b.bytes);
@@ -467,10 +474,17 @@ __device__ __forceinline__ void issue_slab_dma(const BufRef& a, const BufRef& b,
   for (int i = 0; i < A_CNT; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_void_t*)(sA + (i * NW + wave) * 512), 16, a_voff[i], soff, 0,
                                              0);
+  if (b_nt) {
 #pragma unroll
-  for (int i = 0; i < B_PW; ++i)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_void_t*)(sB + (wave * B_PW + i) * 512), 16, b_voff[i], soff, 0,
-                                             0);
+    for (int i = 0; i < B_PW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_void_t*)(sB + (wave * B_PW + i) * 512), 16, b_voff[i], soff,
+                                               0, 2);
+  } else {
+#pragma unroll
+    for (int i = 0; i < B_PW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_void_t*)(sB + (wave * B_PW + i) * 512), 16, b_voff[i], soff,
+                                               0, 0);
+  }
 #endif
 }
 
@@ -627,7 +641,7 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
     for (int i = 0; i < MBE; ++i)
 #pragma unroll
       for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, 0);
+    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, 0, p.b_nt != 0);
     __syncthreads();
     int kt = 0;
     // Slab kt is in buffer 0 at the top of each iteration.  The second load is unconditional
@@ -635,11 +649,12 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_dma_kernel(GemmAr
     // not read again and which the closing barrier waits for) so that it is not split into its
     // own basic block, where the scheduler would queue the previous slab's MFMAs ahead of it.
     for (; kt + 1 < KT; kt += 2) {
-      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA1, sB1, wave, (kt + 1) * BK * 2);
+      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA1, sB1, wave, (kt + 1) * BK * 2, p.b_nt != 0);
       pin_issue();
       slab_mma<G, MBE, F32>(acc, sA0, sB0, wm, wn, lane);
       __syncthreads();
-      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, min(kt + 2, KT - 1) * BK * 2);
+      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, sA0, sB0, wave, min(kt + 2, KT - 1) * BK * 2,
+                                      p.b_nt != 0);
       pin_issue();
       slab_mma<G, MBE, F32>(acc, sA1, sB1, wm, wn, lane);
       __syncthreads();
@@ -1116,15 +1131,15 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8_kernel(GemmAr
     for (int i = 0; i < MBE; ++i)
 #pragma unroll
       for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, a0, b0, wave, 0);
+    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, a0, b0, wave, 0, p.b_nt != 0);
     __syncthreads();
     int kt = 0;
     for (; kt + 1 < KT; kt += 2) {
-      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, a1, b1, wave, (kt + 1) * BKB);
+      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, a1, b1, wave, (kt + 1) * BKB, p.b_nt != 0);
       pin_issue();
       slab_mma_fp8<G, MBE>(acc, sA0, sB0, wm, wn, lane);
       __syncthreads();
-      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, a0, b0, wave, min(kt + 2, KT - 1) * BKB);
+      issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, a0, b0, wave, min(kt + 2, KT - 1) * BKB, p.b_nt != 0);
       pin_issue();
       slab_mma_fp8<G, MBE>(acc, sA1, sB1, wm, wn, lane);
       __syncthreads();
@@ -1354,12 +1369,21 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
     const double avg = static_cast<double>(max_rows) / (p.S > 0 ? p.S : 1);
     return launch_stream_gemm(p, epi, a_fp8, max_rows, avg > 8 ? 2 : 1, s);
   }
-  if (epi == kEpiSiluBF16) return b_fp8 ? launch_epi<kEpiSiluBF16, true>(p, max_rows, tile, a_fp8, s)
-                                        : launch_epi<kEpiSiluBF16, false>(p, max_rows, tile, false, s);
-  if (epi == kEpiStoreBF16) return b_fp8 ? launch_epi<kEpiStoreBF16, true>(p, max_rows, tile, a_fp8, s)
-                                         : launch_epi<kEpiStoreBF16, false>(p, max_rows, tile, false, s);
-  return b_fp8 ? launch_epi<kEpiStoreF32, true>(p, max_rows, tile, a_fp8, s)
-               : launch_epi<kEpiStoreF32, false>(p, max_rows, tile, false, s);
+  // Non-temporal weight DMA on the smaller LDS tiles when a segment's expected rows (with half
+  // again for skew) fit one m-tile, so each weight panel is read once (decode batches).
+  GemmArgs q = p;
+  {
+    const int bm = tile == kTileM ? 128 : tile == kTileS ? 32 : tile == kTileXS ? 16 : 0;
+    const double avg =
+        static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) / (p.S > 0 ? p.S : 1);
+    q.b_nt = bm > 0 && 3.0 * avg <= 2.0 * bm ? 1 : 0;
+  }
+  if (epi == kEpiSiluBF16) return b_fp8 ? launch_epi<kEpiSiluBF16, true>(q, max_rows, tile, a_fp8, s)
+                                        : launch_epi<kEpiSiluBF16, false>(q, max_rows, tile, false, s);
+  if (epi == kEpiStoreBF16) return b_fp8 ? launch_epi<kEpiStoreBF16, true>(q, max_rows, tile, a_fp8, s)
+                                         : launch_epi<kEpiStoreBF16, false>(q, max_rows, tile, false, s);
+  return b_fp8 ? launch_epi<kEpiStoreF32, true>(q, max_rows, tile, a_fp8, s)
+               : launch_epi<kEpiStoreF32, false>(q, max_rows, tile, false, s);
 }
 
 template <int BM, int BN, int WGM, int WGN, int EPI, int GM>

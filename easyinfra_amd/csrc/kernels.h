@@ -39,6 +39,7 @@ struct GemmArgs {
   long long a_rows_cap;      // rows in the A buffer (bounds the buffer resource)
   const float* a_scale;      // fp8 A: per-row dequantisation scale, indexed like A (through a_rows)
   int rows_hint;             // expected rows in the segments (tile choice only); 0: max_rows
+  int b_nt;                  // set by the launcher: weight DMA non-temporal (each weight read by one m-tile)
 };
 
 // Tile shape selector; the launcher maps it to a kernel instantiation.
