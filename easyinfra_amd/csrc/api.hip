@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -133,8 +134,15 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
   const int bm = tile == kTileL ? 256 : tile == kTileM ? 128 : tile == kTileS ? 32 : 16;
   const int bn = gemm_out_cols_per_tile(tile, kEpiStoreF32);
   const int rows = rows_hint > 0 ? std::min(rows_hint, max_rows) : max_rows;
-  const long long mt = std::min<long long>(n_local, rows) + rows / bm;   // m-tiles (bound, or expected)
-  const long long tiles = mt * (H / bn);
+  // m-tiles in full-tile units from the expected rows per segment: whole tiles plus the remainder's
+  // tile, which takes a quarter, half or full height (a short tile costs its share of a round)
+  const int segs = std::max(1, std::min(n_local, rows));
+  const double per = static_cast<double>(rows) / segs;
+  const double rem = per - std::floor(per / bm) * bm;
+  const double rem_tile = rem <= 0.0 ? 0.0 : rem <= bm / 4 ? 0.25 : rem <= bm / 2 ? 0.5 : 1.0;
+  const double mt = segs * (std::floor(per / bm) + rem_tile);
+  const double work = mt * (H / bn);                                              // full-tile units
+  const long long tiles = static_cast<long long>(segs * std::ceil(per / bm)) * (H / bn);   // workgroups
   constexpr double kTileFlops = 4.7e12;   // measured bf16 GEMM rate per CU, FLOP/s
   constexpr double kHbm = 5.0e12;         // achieved HBM rate for plane traffic, B/s
   const double t_tile = 2.0 * bm * bn * static_cast<double>(I) / kTileFlops;
@@ -144,8 +152,8 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
   for (int split = 1; split <= 8; split *= 2) {
     if (I % (64 * split) != 0) break;
     const long long items = tiles * split;
-    const long long rounds = (items + kNumCu - 1) / kNumCu;
-    double cost = static_cast<double>(rounds) / split * t_tile + (split - 1) * t_plane;
+    const double rounds = std::ceil(work * split / kNumCu);
+    double cost = rounds / split * t_tile + (split - 1) * t_plane;
     if (items < 2 * kNumCu && split < 8 && I % (128 * split) == 0) cost = 1e300;   // too few to fill the GPU
     if (cost < best_cost * 0.98) {
       best_cost = cost;

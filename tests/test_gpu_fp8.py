@@ -137,3 +137,28 @@ def test_fp8_mixtral_real_shape(dev, T):
     assert res["w8a16"][1] <= 1e-2 and res["w8a8"][1] <= 1e-2
     assert res["w8a16"][0] <= 5e-2 and res["w8a16"][2] <= 5e-2
     assert res["w8a8"][0] <= 7.5e-2 and res["w8a8"][2] <= 7.5e-2
+
+
+# The W8A8 layer's activation quantisation does not depend on how the routing was obtained or on
+# x's alignment (16-byte aligned rows take the register quantiser, others the two-pass one): the
+# layer routed here, routed by the caller (EIMOE_ROUTING_IN) and run on x 8 bytes past a 16-byte
+# boundary agree bit for bit; 1-256 tokens take the one-workgroup route+align, 300 and 1000 the
+# other routing paths.
+@pytest.mark.parametrize("T", [1, 5, 64, 256, 300, 1000])
+def test_w8a8_layer_same_bytes_whatever_the_routing_path_and_x_alignment(dev, T):
+    inp = make_inputs(SHAPES["mixtral-8x7b-fp8"], T, device="cpu", hidden=256, inter=256)
+    qgu, sgu = oracle.quantize_weights_fp8(inp.w_gate_up.float())
+    qd, sd = oracle.quantize_weights_fp8(inp.w_down.float())
+    x, lg = inp.x.to(dev), inp.logits.to(dev)
+    kw = dict(w_scales=(sgu.to(dev), sd.to(dev)), out_dtype=torch.float32, w8a8=True)
+    out, ids, w = ops.fused_moe(x, lg, 2, qgu.to(dev), qd.to(dev), return_routing=True, **kw)
+    routed_in = ops.fused_moe(x, None, 2, qgu.to(dev), qd.to(dev), routing=(ids, w), num_experts=8, **kw)
+    assert torch.equal(cpu(out), cpu(routed_in))
+    big = torch.empty(T * 256 + 4, dtype=torch.bfloat16, device=dev)
+    x_odd = big[4:].view(T, 256)   # 8 bytes past a 16-byte boundary
+    x_odd.copy_(x)
+    assert x_odd.data_ptr() % 16 == 8
+    odd = ops.fused_moe(x_odd, lg, 2, qgu.to(dev), qd.to(dev), **kw)
+    assert torch.equal(cpu(out), cpu(odd))
+    ref8 = oracle.moe_forward_fp8(inp.x, inp.logits, 2, qgu, sgu, qd, sd, True, mode="w8a8")
+    assert oracle.rel_l2(cpu(out), ref8) <= 1e-2

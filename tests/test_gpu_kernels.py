@@ -311,6 +311,28 @@ def test_combine_matches_index_add(dev, y_dtype, out_dtype, n_split):
     torch.testing.assert_close(cpu(got).float(), ref, rtol=tol, atol=tol)
 
 
+# Batches of up to 512 tokens with slot and split counts up to 8 loads per output vector take a kernel
+# with both fixed (all of a token's loads in flight at once); others the general loop.  Same sums in the same order: a third
+# plane of zeros sends the two-plane case through the general kernel, bit for bit the same output
+# (top-1, 2, 4, 6, 8 with 1 or 2 planes, with and without shared-expert planes, fp32 and bf16 out).
+@pytest.mark.parametrize("k,n_split", [(1, 1), (2, 1), (2, 2), (4, 2), (6, 1), (8, 1)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_combine_fixed_counts_bit_exact_with_general_loop(dev, k, n_split, out_dtype):
+    g = torch.Generator().manual_seed(100 * k + n_split)
+    T, E, H = 301, 12, 256
+    ids = _distinct_ids(T, E, k, g)
+    al = oracle.align(ids.numpy(), 9, 2)            # experts 2..10 local: some slots dropped
+    A = int(al["offsets"][-1])
+    w = torch.rand(T, k, generator=g)
+    y = torch.randn(n_split, A, H, generator=g)
+    pos = torch.as_tensor(al["pos"]).to(dev)
+    for sh in (None, torch.randn(T, H, generator=g).to(dev)):
+        fixed = ops.combine(y.to(dev), pos, w.to(dev), shared_y=sh, out_dtype=out_dtype)
+        y3 = torch.cat([y, torch.zeros(3 - n_split if n_split < 3 else 1, A, H)]).to(dev)
+        general = ops.combine(y3, pos, w.to(dev), shared_y=sh, out_dtype=out_dtype)
+        assert torch.equal(cpu(fixed), cpu(general))
+
+
 # --------------------------------------------------------------------------- GEMMs
 def _segments(counts):
     off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
