@@ -1356,18 +1356,33 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
                                hipStream_t s) {
   if (a_fp8 && !b_fp8) return hipErrorInvalidValue;
-  // The streaming kernel takes bf16 x bf16 or e4m3 x e4m3; fp8 weights with bf16
-  // activations (W8A16) stay on the LDS-tiled kernels.
-  const bool stream_ok = (b_fp8 == a_fp8) && stream_gemm_supported(p, epi, a_fp8);
+  const int ops = !b_fp8 ? 0 : a_fp8 ? 1 : 2;   // the streaming kernel's operand mode
+  const bool stream_ok = stream_gemm_supported(p, epi, ops);
   if (tile == kTileAuto) {
-    tile = gemm_pick_tile(p, epi, b_fp8);
+    if (ops == 2) {
+      // W8A16: the LDS tiles widen the e4m3 weights through registers, the streaming kernel in
+      // registers on the way to the MFMA.  Measured (cold, one box; Mixtral-8x7B 1-64 tokens):
+      // streaming gate/up 49-211 us against 71-207 on 32x128, the down projection (K split 2)
+      // 30-105 against 99-123; 128x128 from 32 expected rows per segment (128 tokens: gate/up 271
+      // vs 307 streamed, down 134 vs 164); the Qwen3-30B-A3B share streams at 32 and 256 tokens
+      // (gate/up 24 / 34 us against 37 / 38 on 32x128).
+      const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) /
+                         (p.S > 0 ? p.S : 1);
+      tile = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
+      if (tile == kTileL && (static_cast<long long>(p.max_rows) / 256 + p.S) * (p.N / gemm_out_cols_per_tile(kTileL, epi)) *
+                                    p.k_split < kNumCu)
+        tile = kTileM;
+      while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) ++tile;
+    } else {
+      tile = gemm_pick_tile(p, epi, b_fp8);
+    }
     // a few rows per segment: stream the weights instead of tiling them through LDS
     if (tile == kTileXS && stream_ok) tile = kTileStream;
   }
   if (tile == kTileStream) {
     if (!stream_ok) return hipErrorInvalidValue;
     const double avg = static_cast<double>(max_rows) / (p.S > 0 ? p.S : 1);
-    return launch_stream_gemm(p, epi, a_fp8, max_rows, avg > 8 ? 2 : 1, s);
+    return launch_stream_gemm(p, epi, ops, max_rows, avg > 8 ? 2 : 1, s);
   }
   // Non-temporal weight DMA on the smaller LDS tiles when a segment's expected rows (with half
   // again for skew) fit one m-tile, so each weight panel is read once (decode batches).

@@ -123,11 +123,12 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
 // Tile for a launch: from the expected rows per segment, the output width and the bytes of
 // one expert's weights (rows_hint/max_rows, p.S, p.N, p.K * p.k_split, nb_rows).
 int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8);
-// Weight-streaming kernel (stream.hip) for segments of a few rows: bf16 x bf16, or
-// e4m3 x e4m3 (fp8 = true, W8A8 with p.a_scale / p.b_scale).
-bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8);
-int stream_out_cols(int N, int epi, bool fp8);   // widest output columns per streaming task (0: unsupported)
-hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s);
+// Weight-streaming kernel (stream.hip) for segments of a few rows.  ops: 0 bf16 x bf16, 1 e4m3 x
+// e4m3 (W8A8, with p.a_scale / p.b_scale), 2 e4m3 weights x bf16 activations (W8A16, p.b_scale).
+bool stream_gemm_supported(const GemmArgs& p, int epi, int ops);
+// widest output columns per streaming task (0: unsupported); fp8: e4m3 weights (128-wide k steps)
+int stream_out_cols(int N, int epi, bool fp8);
+hipError_t launch_stream_gemm(const GemmArgs& p, int epi, int ops, int max_rows, int mblk, hipStream_t s);
 int gemm_out_cols_per_tile(int tile, int epi);
 // fp32 operands on the fp32 MFMA (v_mfma_f32_16x16x4f32): A, B and the output in fp32 (epi
 // kEpiSiluF32 or kEpiStoreF32); LDS-tiled kernels only (tiles 128x128, 32x128, 16x64).

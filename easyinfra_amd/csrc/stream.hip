@@ -23,11 +23,16 @@
 //     re-read from L2, not HBM).
 // MFMA v_mfma_f32_16x16x32_bf16 operand layout: lane l holds row/column l%16 and k
 // 8*(l/16)..+7 of a 32-wide k step; D lane l holds rows 4*(l/16)+r of column l%16.
-// FP8 (W8A8: e4m3 activations and weights, v_mfma_scale_f32_16x16x128_f8f6f4 with unit
-// block scales): one 128-wide k step per 128 bytes of a row, the same byte addresses per
-// lane as the bf16 64-wide step; lane l feeds bytes 16q..+15 and 64+16q..+15 (q = l/16) of
-// both operands, so the k sum is exact whatever order the instruction adds; the per-row
-// activation scale and per-output-channel weight scale are applied in the epilogue.
+// Operand modes (OPS): kOpsBF16 (bf16 x bf16); kOpsW8A8 (e4m3 activations and weights,
+// v_mfma_scale_f32_16x16x128_f8f6f4 with unit block scales): one 128-wide k step per 128 bytes
+// of a row, the same byte addresses per lane as the bf16 64-wide step; lane l feeds bytes
+// 16q..+15 and 64+16q..+15 (q = l/16) of both operands, so the k sum is exact whatever order the
+// instruction adds; the per-row activation scale and per-output-channel weight scale are applied
+// in the epilogue.  kOpsW8A16 (e4m3 weights, bf16 activations, the bf16 MFMA): the weights load as
+// in W8A8, 128 k per step; lane l's 16 weight bytes of each 64-byte half are widened to bf16
+// exactly and feed two 32-wide MFMA steps, and the activations load four 16-byte vectors per step
+// in the same k order (step j covers k (j/2)*64 + 16q + (j%2)*8 + 0..7: every k once); the weight
+// scale is applied in the epilogue.
 #include <algorithm>
 
 #include "common.h"
@@ -95,29 +100,52 @@ __device__ __forceinline__ bool stream_task(const GemmArgs& p, int bm, int n_gro
   return false;
 }
 
-template <int NFRAG, int MBLK>
+enum StreamOps : int { kOpsBF16 = 0, kOpsW8A8 = 1, kOpsW8A16 = 2 };
+constexpr int ops_step_k(int ops) { return ops == kOpsBF16 ? 64 : 128; }   // k per step
+constexpr int ops_a_vecs(int ops) { return ops == kOpsW8A16 ? 4 : 2; }     // 16-byte A vectors per step
+
+template <int NFRAG, int MBLK, int OPS>
 struct StreamStage {
   bf16x8_t b[NFRAG][2];
-  bf16x8_t a[MBLK][2];
+  bf16x8_t a[MBLK][ops_a_vecs(OPS)];
 };
 
-template <int NFRAG, int MBLK>
-__device__ __forceinline__ void stream_load(StreamStage<NFRAG, MBLK>& st, __amdgpu_buffer_rsrc_t ra,
+template <int NFRAG, int MBLK, int OPS>
+__device__ __forceinline__ void stream_load(StreamStage<NFRAG, MBLK, OPS>& st, __amdgpu_buffer_rsrc_t ra,
                                             __amdgpu_buffer_rsrc_t rb, const uint32_t (&a_voff)[MBLK],
                                             const uint32_t (&b_voff)[NFRAG], int step) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const int soff = step * 128;   // 64 bf16 per k step
+  const int soff = step * 128;   // 128 weight bytes of a row per k step
 #pragma unroll
   for (int f = 0; f < NFRAG; ++f)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
       st.b[f][h] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rb, b_voff[f], soff + h * 64, 0));
+  if constexpr (OPS == kOpsW8A16) {
+    // 128 bf16 activations (256 bytes) per step: vector j at (j/2)*128 + (j%2)*16 past the lane's 32q
 #pragma unroll
-  for (int m = 0; m < MBLK; ++m)
+    for (int m = 0; m < MBLK; ++m)
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      st.a[m][h] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[m], soff + h * 64, 0));
+      for (int j = 0; j < 4; ++j)
+        st.a[m][j] = __builtin_bit_cast(
+            bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[m], 2 * soff + (j / 2) * 128 + (j % 2) * 16, 0));
+  } else {
+#pragma unroll
+    for (int m = 0; m < MBLK; ++m)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        st.a[m][h] =
+            __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[m], soff + h * 64, 0));
+  }
 #endif
+}
+
+// Eight e4m3 weights (the low or high half of a 16-byte vector) widened to bf16, exactly.
+__device__ __forceinline__ bf16x8_t widen_fp8x8(const bf16x8_t& v, int half) {
+  const u32x4_t u = __builtin_bit_cast(u32x4_t, v);
+  const u32x2_t lo = fp8x4_to_bf16x4(u[2 * half]);
+  const u32x2_t hi = fp8x4_to_bf16x4(u[2 * half + 1]);
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
 }
 
 __device__ __forceinline__ i32x8_t cat_fp8(const bf16x8_t& lo, const bf16x8_t& hi) {
@@ -126,9 +154,19 @@ __device__ __forceinline__ i32x8_t cat_fp8(const bf16x8_t& lo, const bf16x8_t& h
   return i32x8_t{(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
 }
 
-template <int NFRAG, int MBLK, bool FP8>
-__device__ __forceinline__ void stream_mma(f32x4_t (&acc)[MBLK][NFRAG], const StreamStage<NFRAG, MBLK>& st) {
-  if constexpr (FP8) {
+template <int NFRAG, int MBLK, int OPS>
+__device__ __forceinline__ void stream_mma(f32x4_t (&acc)[MBLK][NFRAG], const StreamStage<NFRAG, MBLK, OPS>& st) {
+  if constexpr (OPS == kOpsW8A16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int f = 0; f < NFRAG; ++f) {
+        const bf16x8_t b = widen_fp8x8(st.b[f][j / 2], j % 2);
+#pragma unroll
+        for (int m = 0; m < MBLK; ++m)
+          acc[m][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.a[m][j], b, acc[m][f], 0, 0, 0);
+      }
+  } else if constexpr (OPS == kOpsW8A8) {
 #pragma unroll
     for (int m = 0; m < MBLK; ++m)
 #pragma unroll
@@ -152,9 +190,9 @@ constexpr int kShortSteps = 4;   // k steps per wave held in flight whole by the
 // EPI kEpiSiluBF16: fragments [0, NFRAG/2) are gate rows col0 + 16f + (0..15), fragments
 // [NFRAG/2, NFRAG) the matching up rows; else NFRAG fragments of 16 consecutive output
 // columns.  W waves split K (the k-step count is a multiple of W*U: the launcher picks W
-// and U; U = 0 is the short-stream mode, at most kShortSteps steps per wave).  FP8: both
-// operands e4m3 (W8A8), 128-wide k steps.
-template <int EPI, int NFRAG, int MBLK, int U, int W, bool FP8>
+// and U; U = 0 is the short-stream mode, at most kShortSteps steps per wave).  OPS: the operand
+// mode (StreamOps).
+template <int EPI, int NFRAG, int MBLK, int U, int W, int OPS>
 __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p) {
   constexpr bool SILU = (EPI == kEpiSiluBF16);
   static_assert(!SILU || NFRAG % 2 == 0, "SiLU pairs gate and up fragments");
@@ -175,10 +213,16 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   const int expert = seg % p.e_mod;
 
   const int lr = lane & 15;
-  const uint32_t kq = static_cast<uint32_t>((lane >> 4) * 16);   // this lane's 16-byte k chunk
-  constexpr int EB = FP8 ? 1 : 2;                                   // bytes per element
+  const uint32_t kq = static_cast<uint32_t>((lane >> 4) * 16);   // this lane's 16-byte weight chunk
+  constexpr bool FP8 = OPS != kOpsBF16;                            // e4m3 weights (128-wide k steps)
+  constexpr bool A8 = OPS == kOpsW8A8;                             // e4m3 activations
+  constexpr int EB = FP8 ? 1 : 2;                                  // bytes per weight
+  constexpr int EA = A8 ? 1 : 2;                                   // bytes per activation
+  // the lane's activation bytes: the same 16-byte chunk as its weights, or, for bf16 activations
+  // against e4m3 weights, the 32 bytes holding the same k
+  const uint32_t kqa = OPS == kOpsW8A16 ? 2 * kq : kq;
   const __amdgpu_buffer_rsrc_t ra =
-      make_rsrc(static_cast<const uint8_t*>(p.a) + k0 * EB, (p.a_rows_cap * p.lda - k0) * EB);
+      make_rsrc(static_cast<const uint8_t*>(p.a) + k0 * EA, (p.a_rows_cap * p.lda - k0) * EA);
   const __amdgpu_buffer_rsrc_t rb =
       make_rsrc(expert_weights(p, expert, EB) + k0 * EB, (p.b_estride - k0) * EB);
   uint32_t a_voff[MBLK], b_voff[NFRAG];
@@ -186,7 +230,7 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   for (int m = 0; m < MBLK; ++m) {
     const int r = min(row0 + m * 16 + lr, row_end - 1);
     const long long src = p.a_rows ? static_cast<long long>(p.a_rows[r]) : static_cast<long long>(r);
-    a_voff[m] = static_cast<uint32_t>(src * p.lda * EB) + kq;
+    a_voff[m] = static_cast<uint32_t>(src * p.lda * EA) + kqa;
   }
   int wrow[NFRAG];
 #pragma unroll
@@ -205,24 +249,24 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   // U divides the step count (the launcher picks it), so the loop body has no branch and
   // the compiler's vmcnt waits stay exact; fetch indices are clamped to the last step, so
   // the final iterations re-read it (L2 hits) instead of branching.
-  const int KW = p.K / (FP8 ? 128 : 64) / W;   // k steps (128 bytes of a row each) of this wave
+  const int KW = p.K / ops_step_k(OPS) / W;   // k steps (128 weight bytes of a row each) of this wave
   const int s0 = wave * KW;
   const int s_last = s0 + KW - 1;
   if constexpr (U == 0) {
     // Short stream (KW <= kShortSteps, small grids): every load of the wave is issued
     // before the first MFMA, so the wave waits for one memory round trip, not KW.
-    StreamStage<NFRAG, MBLK> st[kShortSteps];
+    StreamStage<NFRAG, MBLK, OPS> st[kShortSteps];
 #pragma unroll
     for (int u = 0; u < kShortSteps; ++u)
-      if (u < KW) stream_load<NFRAG, MBLK>(st[u], ra, rb, a_voff, b_voff, s0 + u);
+      if (u < KW) stream_load<NFRAG, MBLK, OPS>(st[u], ra, rb, a_voff, b_voff, s0 + u);
 #pragma unroll
     for (int u = 0; u < kShortSteps; ++u)
-      if (u < KW) stream_mma<NFRAG, MBLK, FP8>(acc, st[u]);
+      if (u < KW) stream_mma<NFRAG, MBLK, OPS>(acc, st[u]);
   } else {
-    StreamStage<NFRAG, MBLK> st[U];
+    StreamStage<NFRAG, MBLK, OPS> st[U];
 #pragma unroll
     for (int u = 0; u < U - 1; ++u) {
-      stream_load<NFRAG, MBLK>(st[u], ra, rb, a_voff, b_voff, min(s0 + u, s_last));
+      stream_load<NFRAG, MBLK, OPS>(st[u], ra, rb, a_voff, b_voff, min(s0 + u, s_last));
 #if defined(__HIP_DEVICE_COMPILE__)
       __builtin_amdgcn_sched_barrier(0);   // stage order must match the loop's for exact vmcnt waits
 #endif
@@ -230,8 +274,8 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
     for (int s = s0; s <= s_last; s += U) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        stream_load<NFRAG, MBLK>(st[(u + U - 1) % U], ra, rb, a_voff, b_voff, min(s + u + U - 1, s_last));
-        stream_mma<NFRAG, MBLK, FP8>(acc, st[u]);
+        stream_load<NFRAG, MBLK, OPS>(st[(u + U - 1) % U], ra, rb, a_voff, b_voff, min(s + u + U - 1, s_last));
+        stream_mma<NFRAG, MBLK, OPS>(acc, st[u]);
 #if defined(__HIP_DEVICE_COMPILE__)
         __builtin_amdgcn_sched_barrier(0);   // keep the ring order: the scheduler would batch all loads
 #endif
@@ -258,8 +302,8 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
   const int lq = lane >> 4;
   // The e4m3 scales are loaded before the first store: loads between stores that may alias
   // them would wait for each other, a chain of memory latencies per row.
-  // bf16 operands carry no scales (the products fold away at compile time); e4m3 operands always
-  // carry both (the W8A8 entry points require them).
+  // bf16 operands carry no scales (the products fold away at compile time); e4m3 weights always
+  // carry their channel scales, e4m3 activations their row scales (the entry points require them).
   float cs[NFRAG];   // per-output-channel weight scales of this lane's fragment columns
   float rsv[MBLK][4];   // per-row activation scales
 #pragma unroll
@@ -273,12 +317,12 @@ __global__ void __launch_bounds__(64 * W) grouped_gemm_stream_kernel(GemmArgs p)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = min(row0 + m * 16 + lq * 4 + r, row_end - 1);
-      src_row[m][r] = FP8 ? (p.a_rows ? p.a_rows[row] : row) : 0;
+      src_row[m][r] = A8 ? (p.a_rows ? p.a_rows[row] : row) : 0;
     }
 #pragma unroll
   for (int m = 0; m < MBLK; ++m)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) rsv[m][r] = FP8 ? p.a_scale[src_row[m][r]] : 1.f;
+    for (int r = 0; r < 4; ++r) rsv[m][r] = A8 ? p.a_scale[src_row[m][r]] : 1.f;
 #pragma unroll
   for (int m = 0; m < MBLK; ++m) {
 #pragma unroll
@@ -322,24 +366,24 @@ long long stream_tasks_bound(const GemmArgs& p, int max_rows, int nfrag, int mbl
   return chunks * (p.N / cols) * p.k_split;
 }
 
-template <int EPI, int NFRAG, int MBLK, int W, bool FP8>
+template <int EPI, int NFRAG, int MBLK, int W, int OPS>
 hipError_t launch_stream_short(const GemmArgs& p, dim3 g, hipStream_t s) {
-  hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 0, W, FP8>), g, dim3(64 * W), 0, s, p);
+  hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 0, W, OPS>), g, dim3(64 * W), 0, s, p);
   return hipGetLastError();
 }
 
-template <int EPI, int NFRAG, int MBLK, int W, bool FP8>
+template <int EPI, int NFRAG, int MBLK, int W, int OPS>
 hipError_t launch_stream_w(const GemmArgs& p, dim3 g, hipStream_t s) {
   const dim3 b(64 * W);
-  if ((p.K / (FP8 ? 128 : 64) / W) % 2 == 0)
-    hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 2, W, FP8>), g, b, 0, s, p);
+  if ((p.K / ops_step_k(OPS) / W) % 2 == 0)
+    hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 2, W, OPS>), g, b, 0, s, p);
   else
-    hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 1, W, FP8>), g, b, 0, s, p);
+    hipLaunchKernelGGL((grouped_gemm_stream_kernel<EPI, NFRAG, MBLK, 1, W, OPS>), g, b, 0, s, p);
   return hipGetLastError();
 }
 
 // Grid from the row bound; the K split from the expected rows (rows_hint) when given.
-template <int EPI, int NFRAG, int MBLK, bool FP8>
+template <int EPI, int NFRAG, int MBLK, int OPS>
 hipError_t launch_stream_cfg(const GemmArgs& p, int max_rows, int rows, hipStream_t s) {
   const long long grid = stream_tasks_bound(p, max_rows, NFRAG, MBLK, EPI);
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
@@ -347,26 +391,26 @@ hipError_t launch_stream_cfg(const GemmArgs& p, int max_rows, int rows, hipStrea
   const long long tasks = stream_tasks_bound(p, rows, NFRAG, MBLK, EPI);
   // Split K over the workgroup's waves only while each wave keeps >= 16 steps: shorter
   // streams spend a large share of their time filling and draining the register ring.
-  const int ks = p.K / (FP8 ? 128 : 64);
+  const int ks = p.K / ops_step_k(OPS);
   const int w = (ks % 4 == 0 && ks / 4 >= 16) ? 4 : (ks % 2 == 0 && ks / 2 >= 16) ? 2 : 1;
   if constexpr (NFRAG == 2) {
     // Grids of fewer than ~8 waves per CU (a few tokens) are latency-bound: each wave's
     // stream is a chain of memory round trips.  Split K over 4 or 8 waves so each holds
     // at most kShortSteps steps, all in flight at once.
     if (tasks * w < 8ll * kNumCu) {
-      if (ks % 4 == 0 && ks / 4 <= kShortSteps) return launch_stream_short<EPI, NFRAG, MBLK, 4, FP8>(p, g, s);
-      if (ks % 8 == 0 && ks / 8 <= kShortSteps) return launch_stream_short<EPI, NFRAG, MBLK, 8, FP8>(p, g, s);
+      if (ks % 4 == 0 && ks / 4 <= kShortSteps) return launch_stream_short<EPI, NFRAG, MBLK, 4, OPS>(p, g, s);
+      if (ks % 8 == 0 && ks / 8 <= kShortSteps) return launch_stream_short<EPI, NFRAG, MBLK, 8, OPS>(p, g, s);
     }
   }
-  if (w == 4) return launch_stream_w<EPI, NFRAG, MBLK, 4, FP8>(p, g, s);
-  if (w == 2) return launch_stream_w<EPI, NFRAG, MBLK, 2, FP8>(p, g, s);
-  return launch_stream_w<EPI, NFRAG, MBLK, 1, FP8>(p, g, s);
+  if (w == 4) return launch_stream_w<EPI, NFRAG, MBLK, 4, OPS>(p, g, s);
+  if (w == 2) return launch_stream_w<EPI, NFRAG, MBLK, 2, OPS>(p, g, s);
+  return launch_stream_w<EPI, NFRAG, MBLK, 1, OPS>(p, g, s);
 }
 
-template <int EPI, int NFRAG, bool FP8>
+template <int EPI, int NFRAG, int OPS>
 hipError_t launch_stream_nf(const GemmArgs& p, int max_rows, int rows, int mblk, hipStream_t s) {
-  return mblk == 1 ? launch_stream_cfg<EPI, NFRAG, 1, FP8>(p, max_rows, rows, s)
-                   : launch_stream_cfg<EPI, NFRAG, 2, FP8>(p, max_rows, rows, s);
+  return mblk == 1 ? launch_stream_cfg<EPI, NFRAG, 1, OPS>(p, max_rows, rows, s)
+                   : launch_stream_cfg<EPI, NFRAG, 2, OPS>(p, max_rows, rows, s);
 }
 
 // Fragments per wave: as many as the output width allows, up to 8 (each activation load
@@ -385,8 +429,8 @@ int stream_nfrag(const GemmArgs& p, int epi, int max_rows, int mblk, bool fp8) {
 
 }  // namespace
 
-bool stream_gemm_supported(const GemmArgs& p, int epi, bool fp8) {
-  return p.K % (fp8 ? 128 : 64) == 0 && stream_nfrag(p, epi, 0, 1, fp8) > 0;
+bool stream_gemm_supported(const GemmArgs& p, int epi, int ops) {
+  return p.K % ops_step_k(ops) == 0 && stream_nfrag(p, epi, 0, 1, ops != kOpsBF16) > 0;
 }
 
 int stream_out_cols(int N, int epi, bool fp8) {
@@ -396,24 +440,24 @@ int stream_out_cols(int N, int epi, bool fp8) {
   return 0;
 }
 
-hipError_t launch_stream_gemm(const GemmArgs& p, int epi, bool fp8, int max_rows, int mblk, hipStream_t s) {
+hipError_t launch_stream_gemm(const GemmArgs& p, int epi, int ops, int max_rows, int mblk, hipStream_t s) {
   const int rows = p.rows_hint > 0 ? std::min(p.rows_hint, max_rows) : max_rows;   // expected rows
-  const int nf = stream_nfrag(p, epi, rows, mblk, fp8);
-  if (p.K % (fp8 ? 128 : 64) != 0 || nf == 0) return hipErrorInvalidValue;
-#define EIMOE_STREAM_NF(E, F8)                                               \
-  switch (nf) {                                                              \
-    case 8: return launch_stream_nf<E, 8, F8>(p, max_rows, rows, mblk, s);   \
-    case 4: return launch_stream_nf<E, 4, F8>(p, max_rows, rows, mblk, s);   \
-    default: return launch_stream_nf<E, 2, F8>(p, max_rows, rows, mblk, s);  \
+  const int nf = stream_nfrag(p, epi, rows, mblk, ops != kOpsBF16);
+  if (p.K % ops_step_k(ops) != 0 || nf == 0) return hipErrorInvalidValue;
+#define EIMOE_STREAM_NF(E, O)                                               \
+  switch (nf) {                                                             \
+    case 8: return launch_stream_nf<E, 8, O>(p, max_rows, rows, mblk, s);   \
+    case 4: return launch_stream_nf<E, 4, O>(p, max_rows, rows, mblk, s);   \
+    default: return launch_stream_nf<E, 2, O>(p, max_rows, rows, mblk, s);  \
   }
-  if (fp8) {
-    if (epi == kEpiSiluBF16) { EIMOE_STREAM_NF(kEpiSiluBF16, true) }
-    if (epi == kEpiStoreBF16) { EIMOE_STREAM_NF(kEpiStoreBF16, true) }
-    EIMOE_STREAM_NF(kEpiStoreF32, true)
-  }
-  if (epi == kEpiSiluBF16) { EIMOE_STREAM_NF(kEpiSiluBF16, false) }
-  if (epi == kEpiStoreBF16) { EIMOE_STREAM_NF(kEpiStoreBF16, false) }
-  EIMOE_STREAM_NF(kEpiStoreF32, false)
+#define EIMOE_STREAM_EPI(O)                                           \
+  if (epi == kEpiSiluBF16) { EIMOE_STREAM_NF(kEpiSiluBF16, O) }      \
+  if (epi == kEpiStoreBF16) { EIMOE_STREAM_NF(kEpiStoreBF16, O) }    \
+  EIMOE_STREAM_NF(kEpiStoreF32, O)
+  if (ops == kOpsW8A8) { EIMOE_STREAM_EPI(kOpsW8A8) }
+  if (ops == kOpsW8A16) { EIMOE_STREAM_EPI(kOpsW8A16) }
+  EIMOE_STREAM_EPI(kOpsBF16)
+#undef EIMOE_STREAM_EPI
 #undef EIMOE_STREAM_NF
 }
 

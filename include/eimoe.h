@@ -59,9 +59,10 @@ enum {
 };
 
 /* tile selector for the GEMM entry points (0 = automatic).  EIMOE_TILE_STREAM is the
- * weight-streaming kernel for a few rows per segment (bf16 weights only; K % 64 == 0 and the
- * output columns a multiple of 16 for gate/up, 32 otherwise); automatic selection uses it
- * for bf16 weights when the average rows per segment are below 24. */
+ * weight-streaming kernel for a few rows per segment (bf16 weights with K % 64 == 0, or e4m3
+ * weights with K % 128 == 0 and bf16 or, in the W8A8 entry points, e4m3 activations; the output
+ * columns a multiple of 16 for gate/up, 32 otherwise); automatic selection uses it when the
+ * average rows per segment are small. */
 enum { EIMOE_TILE_AUTO = 0, EIMOE_TILE_256x256 = 1, EIMOE_TILE_128x128 = 2, EIMOE_TILE_32x128 = 3,
        EIMOE_TILE_16x64 = 4, EIMOE_TILE_STREAM = 5 };
 

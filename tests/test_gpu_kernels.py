@@ -610,6 +610,40 @@ def test_fp8_weight_gemms(dev, tile):
         torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
 
 
+# W8A16 on the weight-streaming kernel (tile 5): e4m3 weights widened to bf16 in registers against
+# bf16 activations, 128 k per step.  The shapes reach its short-stream mode (H 256; the 1024-wide
+# down projection), the 2- and 4-wave K splits with a 2-deep register ring (H 4096, 8192) and the
+# unsplit ring (the 256-wide down projection); gathered rows, row chunks past 32, empty and one-row
+# segments.
+@pytest.mark.parametrize("H,I,counts", [(256, 256, [20, 0, 70, 1]), (4096, 1024, [40, 3, 0, 90]),
+                                        (8192, 256, [33, 1, 64, 0, 7])])
+def test_fp8_weight_stream_gemms(dev, H, I, counts):
+    g = torch.Generator().manual_seed(H + I)
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 50
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
+    wgu = torch.randn(E, 2 * I, H, generator=g) * 0.02
+    wd = torch.randn(E, H, I, generator=g) * 0.02
+    qgu, sgu = oracle.quantize_weights_fp8(wgu)
+    qd, sd = oracle.quantize_weights_fp8(wd)
+    h = ops.gemm_gate_up_silu(x.to(dev), qgu.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev), w_scale=sgu.to(dev),
+                              tile=5)
+    y = ops.gemm_down(h, qd.to(dev), off_t.to(dev), rows, w_scale=sd.to(dev), tile=5)
+    h, y = cpu(h).float(), cpu(y)[0]
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        gu = (x[a_rows[a:b].long()].float() @ qgu[e].float().T) * sgu[e]
+        href = oracle.silu(gu[:, :I]) * gu[:, I:]
+        torch.testing.assert_close(h[a:b], href, rtol=1e-2, atol=1e-2)
+        yref = (h[a:b] @ qd[e].float().T) * sd[e]
+        torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
+
+
 # Segment remainders of every height class: a segment's last tile is a quarter, half or full
 # tile (256x256: 64 / 128 / 256 rows; 128x128: 32 / 64 / 128), and the last m-tile group of a
 # long segment takes the leftover tiles (10 m-tiles of 256 rows: groups of 4 and 6).
