@@ -470,7 +470,7 @@ def main():
     gu_ms = stages["gate_up_silu"]
     achieved = gu_flops / (gu_ms * 1e-3) / 1e12
     traffic, traffic_src = traffic_from_profiles("gate_up_silu_prefill")
-    roof = {"bound": "mfma", "kernel": "grouped_gemm_pp3p_kernel<2,8,false> (256x256 bf16 gate/up + SiLU*mul, persistent)",
+    roof = {"bound": "mfma", "kernel": "grouped_gemm_pp3p_kernel<2, 8, 0> (256x256 bf16 gate/up + SiLU*mul, persistent)",
             "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
             "flops_per_launch": gu_flops, "mean_launch_ms": round(gu_ms, 4),

@@ -820,8 +820,9 @@ struct PpStages {
   uint16_t *a0, *a1, *b0, *b1, *b2;
 };
 
-// Operand windows and per-lane B offsets of one 256x256 ping-pong tile.
-template <class G, int EB, int FR = 16>
+// Operand windows and per-lane B offsets of one 256x256 ping-pong tile; EB bytes per weight, EA
+// per activation (bf16 activations against e4m3 weights in W8A16).
+template <class G, int EB, int FR = 16, int EA = EB>
 struct PpOperands {
   static constexpr int B_PW = 256 / 8 / G::NW;
   BufRef rA, rB;
@@ -831,7 +832,7 @@ struct PpOperands {
     // uniform by construction, taken from the first lane so that the compiler keeps them in
     // SGPRs: in the persistent kernel's tile loop it could not prove it and wrapped every
     // buffer load in a readfirstlane loop (measured: MFMA busy 63 % against 79 %)
-    rA = BufRef{uniform(static_cast<const uint8_t*>(p.a) + k0 * EB), uniform((p.a_rows_cap * p.lda - k0) * EB)};
+    rA = BufRef{uniform(static_cast<const uint8_t*>(p.a) + k0 * EA), uniform((p.a_rows_cap * p.lda - k0) * EA)};
     rB = BufRef{uniform(expert_weights(p, tc.expert, EB) + k0 * EB), uniform((p.b_estride - k0) * EB)};
 #pragma unroll
     for (int i = 0; i < B_PW; ++i) {
@@ -898,6 +899,108 @@ __device__ __forceinline__ void pp3_kloop(f32x4_t (&acc)[MBE][G::NB], const BufR
   }
 #undef EIMOE_PP3_SLAB
 #undef EIMOE_PP3_HALF
+  if (grp == 0) pp_barrier();   // matches group 1's late start: every wave has read its last slab
+}
+
+// Eight e4m3 weights (two 32-bit words, bytes in k order) widened to bf16 with gfx950's
+// v_cvt_scalef32_pk_bf16_fp8 at scale 1: exact (e4m3 values are bf16 values), and bit-identical to
+// widening through fp32 on all 65536 byte pairs (NaNs included; compared on gfx950).
+__device__ __forceinline__ bf16x8_t widen_fp8x8(uint32_t w0, uint32_t w1) {
+  const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w0), 1.0f, false);
+  const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w0), 1.0f, true);
+  const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w1), 1.0f, false);
+  const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w1), 1.0f, true);
+  return bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// The K loop of the W8A16 ping-pong tile: bf16 activations against e4m3 weights on the bf16 MFMA.
+// A stage is a 64-wide k slab of activations (128-byte rows of bf16, as for bf16); a B stage holds
+// 128 k of weights (128-byte rows of e4m3), so weight chunk c serves slabs 2c and 2c+1 and its DMA
+// runs every other slab: chunk c+2 goes out in the second phase of slab 2c+1, into the stage of
+// chunk c-1.  Within a slab lane group q takes k = 16q + 8*KK + (0..7) in phase KK (every k once):
+// its activation fragment is chunk 2q+KK of the row, and one 16-byte weight read per slab in phase
+// 0 (chunk 4*(slab%2) + q) covers both phases, widened half by half.  So each slab reads 16 1-KiB
+// LDS blocks per wave instead of 24 and fetches half the weight bytes.  Slab ends wait for all but
+// the latest B DMA after an odd slab (vmcnt(4)), for everything after an even one (the chunk issued
+// a slab earlier is then complete 1.5 slabs after its issue, as the bf16 loop's B).  K % 128 == 0.
+template <class G, int MBE, int A_CNT, int A_PW, int B_PW>
+__device__ __forceinline__ void pp3w_kloop(f32x4_t (&acc)[MBE][G::NB], const BufRef& rA, const BufRef& rB,
+                                           const uint32_t (&a_voff)[A_PW], const uint32_t (&b_voff)[B_PW], int KT,
+                                           int wave, int lane, const PpStages& st) {
+  constexpr int NW = G::NW;
+  const int grp = wave >> 2;
+  const int wm = wave % 4;
+  const int wn = wave / 4;
+  const int lr = lane & 15;
+  const int q = lane >> 4;
+  const int NC = KT / 2;   // 128-k weight chunks
+  uint16_t* const sA0 = st.a0;
+  uint16_t* const sA1 = st.a1;
+  uint16_t* const sB0 = st.b0;
+  uint16_t* const sB1 = st.b1;
+  uint16_t* const sB2 = st.b2;
+  if (grp == 1) pp_barrier();
+  bf16x8_t af[MBE], bw[G::NB];
+  u32x4_t braw[G::NB];
+  auto read_a = [&](const uint16_t* sA, int KK) {
+#pragma unroll
+    for (int i = 0; i < MBE; ++i) {
+      const int R = wm * 16 * MBE + i * 16 + lr;
+      af[i] = *reinterpret_cast<const bf16x8_t*>(&sA[R * G::BK + (((2 * q + KK) ^ swz(R)) << 3)]);
+    }
+  };
+  auto read_b = [&](const uint16_t* sB, int half) {
+    const uint8_t* b8 = reinterpret_cast<const uint8_t*>(sB);
+#pragma unroll
+    for (int j = 0; j < G::NB; ++j) {
+      const int R = wn * G::WN + j * 16 + lr;
+      braw[j] = *reinterpret_cast<const u32x4_t*>(&b8[R * 128 + (((4 * half + q) ^ swz(R)) << 4)]);
+    }
+  };
+  auto widen = [&](int KK) {
+#pragma unroll
+    for (int j = 0; j < G::NB; ++j) bw[j] = widen_fp8x8(braw[j][2 * KK], braw[j][2 * KK + 1]);
+  };
+  // slab kt + J reads activations from SA and weights from SB (its chunk's stage); loads A(kt+J+1)
+  // into SAN and, for odd J, weight chunk (kt+J)/2 + 2 into SBN (clamped near the end: those
+  // stages are not read again)
+#define EIMOE_PPW_SLAB(J, SA, SB, SAN, SBN)                                                          \
+  if (kt + J < KT) {                                                                                 \
+    issue_a_dma<A_CNT, NW>(rA, a_voff, SAN, wave, min(kt + J + 1, KT - 1) * 128);                    \
+    read_a(SA, 0);                                                                                   \
+    read_b(SB, J % 2);                                                                               \
+    pp_wait_lgkm0();                                                                                 \
+    widen(0);                                                                                        \
+    pp_barrier();                                                                                    \
+    mma<G, MBE>(acc, af, bw);                                                                        \
+    pp_barrier();                                                                                    \
+    if (J % 2 == 1)                                                                                  \
+      issue_ab_dma<0, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, 0,                           \
+                                min((kt + J) / 2 + 2, NC - 1) * 128);                                \
+    read_a(SA, 1);                                                                                   \
+    widen(1);                                                                                        \
+    pp_wait_lgkm0();                                                                                 \
+    if (grp == 1) {                                                                                  \
+      if (J % 2 == 1) pp_wait_vm4();                                                                 \
+      else pp_wait_vm0();                                                                            \
+    }                                                                                                \
+    pp_barrier();                                                                                    \
+    mma<G, MBE>(acc, af, bw);                                                                        \
+    if (grp == 0) {                                                                                  \
+      if (J % 2 == 1) pp_wait_vm4();                                                                 \
+      else pp_wait_vm0();                                                                            \
+    }                                                                                                \
+    pp_barrier();                                                                                    \
+  }
+  for (int kt = 0; kt < KT; kt += 6) {
+    EIMOE_PPW_SLAB(0, sA0, sB0, sA1, sB2)
+    EIMOE_PPW_SLAB(1, sA1, sB0, sA0, sB2)
+    EIMOE_PPW_SLAB(2, sA0, sB1, sA1, sB0)
+    EIMOE_PPW_SLAB(3, sA1, sB1, sA0, sB0)
+    EIMOE_PPW_SLAB(4, sA0, sB2, sA1, sB1)
+    EIMOE_PPW_SLAB(5, sA1, sB2, sA0, sB1)
+  }
+#undef EIMOE_PPW_SLAB
   if (grp == 0) pp_barrier();   // matches group 1's late start: every wave has read its last slab
 }
 
@@ -984,11 +1087,16 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3_kernel(GemmArgs p) {
 // no wave reads any more once the K loop's last barrier has passed.  Every workgroup's loop is
 // bounded by its share of the tiles.  Same tiles, DMA and accumulation order as
 // grouped_gemm_pp3_kernel: bit-identical results.
-template <int EPI, int GM, bool FP8 = false>
+// MODE: 0 bf16 x bf16, 1 W8A8 (e4m3 x e4m3 on the fp8 MFMA), 2 W8A16 (bf16 activations x e4m3
+// weights on the bf16 MFMA, pp3w_kloop; K % 128 == 0).
+template <int EPI, int GM, int MODE = 0>
 __global__ void __launch_bounds__(512) grouped_gemm_pp3p_kernel(GemmArgs p) {
   using G = Geo<256, 256, 4, 2, EPI>;
   constexpr int BK = G::BK;
-  constexpr int EB = FP8 ? 1 : 2;
+  constexpr bool FP8 = MODE == 1;    // e4m3 activations and weights
+  constexpr bool WFP8 = MODE != 0;   // e4m3 weights (per-channel scales)
+  constexpr int EB = WFP8 ? 1 : 2;   // bytes per weight
+  constexpr int EA = FP8 ? 1 : 2;    // bytes per activation
   constexpr int NW = G::NW;
   constexpr int A_PW = 256 / 8 / G::NW;
   constexpr int B_PW = 256 / 8 / G::NW;
@@ -1005,7 +1113,8 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3p_kernel(GemmArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave % 4;
   const int wn = wave / 4;
-  const int KT = p.K * EB / (BK * 2);
+  const int KT = p.K * EA / (BK * 2);        // 128-byte activation slabs
+  const int B1 = MODE == 2 ? min(1, KT / 2 - 1) : min(1, KT - 1);   // the B stage loaded second
   const RegSched rsch = reg_sched<256, G::OUT_BN>(p, lane);
   const int xcd = blockIdx.x % kNumXcd;
   const int stride = gridDim.x / kNumXcd;   // the launch rounds the grid to whole XCD rounds
@@ -1017,18 +1126,19 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3p_kernel(GemmArgs p) {
   // first tile: its row map, scales and first slabs (every A block: a short tile's extra rows
   // repeat its last row and are not read)
   uint32_t a_voff[A_PW];
-  a_offsets<A_PW, NW>(p, tc, wave, lane, EB, a_voff);
+  a_offsets<A_PW, NW>(p, tc, wave, lane, EA, a_voff);
+  const float* const a_scale = FP8 ? p.a_scale : nullptr;
   EpiScales<G, MB> sc;
   {
-    const PpOperands<G, EB> op(p, tc, wave, lane);
-    const float* scale = FP8 ? p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows : nullptr;
+    const PpOperands<G, EB, 16, EA> op(p, tc, wave, lane);
+    const float* scale = WFP8 ? p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows : nullptr;
     int src_row[MB][4];
-    if constexpr (FP8)
-      epi_load_scales_1<G, MB>(p, tc, wm, wn, lane, scale, p.a_scale, sc, src_row,
+    if constexpr (WFP8)
+      epi_load_scales_1<G, MB>(p, tc, wm, wn, lane, scale, a_scale, sc, src_row,
                                mbe_of_rows<256, MB, A_PW>(tc.row_end - tc.row0));
     issue_ab_dma<A_PW, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB0, wave, 0, 0);
-    issue_ab_dma<0, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
-    if constexpr (FP8) epi_load_scales_2<G, MB>(p.a_scale, sc, src_row);
+    issue_ab_dma<0, B_PW, NW>(op.rA, op.rB, a_voff, op.b_voff, sA0, sB1, wave, 0, B1 * BK * 2);
+    if constexpr (WFP8) epi_load_scales_2<G, MB>(a_scale, sc, src_row);
   }
   for (;;) {
     TileCoord tn;
@@ -1046,32 +1156,33 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3p_kernel(GemmArgs p) {
       for (int i = 0; i < MBE; ++i)
 #pragma unroll
         for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const PpOperands<G, EB> op(p, tc, wave, lane);
+      const PpOperands<G, EB, 16, EA> op(p, tc, wave, lane);
       pp_wait_vm0();   // this tile's first slabs and scales (and the previous tile's stores)
-      if constexpr (FP8) pin_scales(sc);
+      if constexpr (WFP8) pin_scales(sc);
       pp_barrier();
       // the next tile's row map: in flight during the first slab, whose end wait covers it
       uint32_t an_voff[A_PW];
-      if (more) a_offsets<A_PW, NW>(p, tn, wave, lane, EB, an_voff);
-      pp3_kloop<FP8, G, MBE, A_CNT>(acc, op.rA, op.rB, a_voff, op.b_voff, KT, wave, lane, st);
+      if (more) a_offsets<A_PW, NW>(p, tn, wave, lane, EA, an_voff);
+      if constexpr (MODE == 2) pp3w_kloop<G, MBE, A_CNT>(acc, op.rA, op.rB, a_voff, op.b_voff, KT, wave, lane, st);
+      else pp3_kloop<FP8, G, MBE, A_CNT>(acc, op.rA, op.rB, a_voff, op.b_voff, KT, wave, lane, st);
       pp_wait_vm0();   // this wave's clamped loads have landed in its own LDS blocks
       EpiScales<G, MB> sn;
       if (more) {
-        const PpOperands<G, EB> on(p, tn, wave, lane);
-        const float* scale_n = FP8 ? p.b_scale + static_cast<long long>(tn.expert) * p.nb_rows : nullptr;
+        const PpOperands<G, EB, 16, EA> on(p, tn, wave, lane);
+        const float* scale_n = WFP8 ? p.b_scale + static_cast<long long>(tn.expert) * p.nb_rows : nullptr;
         int src_row[MB][4];
-        if constexpr (FP8)
-          epi_load_scales_1<G, MB>(p, tn, wm, wn, lane, scale_n, p.a_scale, sn, src_row,
+        if constexpr (WFP8)
+          epi_load_scales_1<G, MB>(p, tn, wm, wn, lane, scale_n, a_scale, sn, src_row,
                                    mbe_of_rows<256, MB, A_PW>(tn.row_end - tn.row0));
         issue_ab_dma<A_PW, B_PW, NW>(on.rA, on.rB, an_voff, on.b_voff, sA0, sB0, wave, 0, 0);
-        issue_ab_dma<0, B_PW, NW>(on.rA, on.rB, an_voff, on.b_voff, sA0, sB1, wave, 0, min(1, KT - 1) * BK * 2);
-        if constexpr (FP8) epi_load_scales_2<G, MB>(p.a_scale, sn, src_row);
+        issue_ab_dma<0, B_PW, NW>(on.rA, on.rB, an_voff, on.b_voff, sA0, sB1, wave, 0, B1 * BK * 2);
+        if constexpr (WFP8) epi_load_scales_2<G, MB>(a_scale, sn, src_row);
 #pragma unroll
         for (int i = 0; i < A_PW; ++i) a_voff[i] = an_voff[i];
       }
-      if constexpr (FP8) epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, sc);
+      if constexpr (WFP8) epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, sc);
       else epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr, nullptr);
-      if constexpr (FP8) sc = sn;
+      if constexpr (WFP8) sc = sn;
     });
     if (!more) break;
     tc = tn;
@@ -1255,8 +1366,13 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
 // Tile grouping depth 8: on the current kernels (persistent tile walk, hardware-reciprocal SiLU)
 // depth 8 and 16 both run the Mixtral-8x7B 8192-token layer ~1 % faster than 4 (4.25 vs 4.29 ms,
 // W8A8 2.40-2.42 vs 2.43-2.44 ms; DeepSeek-V2-Lite within noise, two repeats on one box).
-template <int EPI, bool FP8 = false, int GMX = 8>
+// MODE as grouped_gemm_pp3p_kernel's.  W8A16 runs the ping-pong kernel persistent only (launches
+// of at most 64 segments, K % 128 == 0); otherwise the lock-step kernel that widens the weights
+// through registers.
+template <int EPI, int MODE = 0, int GMX = 8>
 static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
+  if constexpr (MODE == 2)
+    if (p.S > 64 || p.K % 128 != 0) return launch_cfg<256, 256, 4, 2, EPI, true, 4>(p, max_rows, false, s);
   constexpr int OUT_BN = epi_silu(EPI) ? 128 : 256;
   const int n_tiles = p.N / OUT_BN;
   const long long max_mt = (static_cast<long long>(max_rows) + 255) / 256 + p.S;
@@ -1270,12 +1386,14 @@ static hipError_t launch_pp(const GemmArgs& p, int max_rows, hipStream_t s) {
     // under counters, layers within 0-1 % (the bf16 GEMMs run at the chip's power-limited clock
     // either way, so hiding the per-tile latencies buys them nothing).
     const long long pgrid = std::min<long long>(grid, kNumCu);
-    hipLaunchKernelGGL((grouped_gemm_pp3p_kernel<EPI, GMX, FP8>), dim3(static_cast<unsigned>(pgrid)), dim3(512), 0, s,
-                       p);
+    hipLaunchKernelGGL((grouped_gemm_pp3p_kernel<EPI, GMX, MODE>), dim3(static_cast<unsigned>(pgrid)), dim3(512), 0,
+                       s, p);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((grouped_gemm_pp3_kernel<EPI, GMX, FP8>), dim3(static_cast<unsigned>(grid)), dim3(512), 0, s,
-                     p);
+  if constexpr (MODE != 2) {
+    hipLaunchKernelGGL((grouped_gemm_pp3_kernel<EPI, GMX, MODE == 1>), dim3(static_cast<unsigned>(grid)), dim3(512),
+                       0, s, p);
+  }
   return hipGetLastError();
 }
 
@@ -1284,10 +1402,10 @@ static hipError_t launch_epi(const GemmArgs& p, int max_rows, int tile, bool a_f
   switch (tile) {
     case kTileL:
       if constexpr (BFP8) {
-        if (a_fp8) return launch_pp<EPI, true>(p, max_rows, s);
-        return launch_cfg<256, 256, 4, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
+        if (a_fp8) return launch_pp<EPI, 1>(p, max_rows, s);
+        return launch_pp<EPI, 2>(p, max_rows, s);
       } else {
-        return launch_pp<EPI>(p, max_rows, s);
+        return launch_pp<EPI, 0>(p, max_rows, s);
       }
     case kTileM: return launch_cfg<128, 128, 2, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
     case kTileS: return launch_cfg<32, 128, 1, 4, EPI, BFP8, 1>(p, max_rows, a_fp8, s);

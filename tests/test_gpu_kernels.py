@@ -644,6 +644,44 @@ def test_fp8_weight_stream_gemms(dev, H, I, counts):
         torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
 
 
+# W8A16 on the 256x256 ping-pong tile (e4m3 weights DMA'd to LDS, 128 k per stage, widened at
+# fragment reads): quarter, half and full-height tiles and several m-tiles per segment, gathered
+# rows, K of one 128-k weight chunk (H 128), of exactly one unrolled loop (6 slabs: H 384, the down
+# projection's 768 split in two) and not a multiple of it (H 1024: 16 slabs; 768 unsplit: 12).
+@pytest.mark.parametrize("H,I,k_split", [(128, 256, 1), (384, 256, 1), (1024, 256, 1), (512, 768, 1),
+                                         (512, 768, 2)])
+def test_fp8_weight_pingpong_gemms(dev, H, I, k_split):
+    g = torch.Generator().manual_seed(H + I + k_split)
+    counts = [257, 320, 63, 0, 129, 2 * 256 + 2, 64]
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 300
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
+    wgu = torch.randn(E, 2 * I, H, generator=g) * 0.02
+    wd = torch.randn(E, H, I, generator=g) * 0.02
+    qgu, sgu = oracle.quantize_weights_fp8(wgu)
+    qd, sd = oracle.quantize_weights_fp8(wd)
+    hs = (torch.randn(rows, I, generator=g) * 0.5).to(torch.bfloat16)
+    h = cpu(ops.gemm_gate_up_silu(x.to(dev), qgu.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev),
+                                  w_scale=sgu.to(dev), tile=1)).float()
+    down = H % 256 == 0   # the 256x256 down tile writes 256 output columns
+    if down:
+        y = cpu(ops.gemm_down(hs.to(dev), qd.to(dev), off_t.to(dev), rows, w_scale=sd.to(dev), k_split=k_split,
+                              tile=1)).sum(0)
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        gu = (x[a_rows[a:b].long()].float() @ qgu[e].float().T) * sgu[e]
+        href = oracle.silu(gu[:, :I]) * gu[:, I:]
+        torch.testing.assert_close(h[a:b], href, rtol=1e-2, atol=1e-2)
+        if down:
+            yref = (hs[a:b].float() @ qd[e].float().T) * sd[e]
+            torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
+
+
 # Segment remainders of every height class: a segment's last tile is a quarter, half or full
 # tile (256x256: 64 / 128 / 256 rows; 128x128: 32 / 64 / 128), and the last m-tile group of a
 # long segment takes the leftover tiles (10 m-tiles of 256 rows: groups of 4 and 6).
