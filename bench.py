@@ -54,7 +54,7 @@ def parse():
                     help="skip the other workloads (tiny fp32 layer, DeepSeek-V2-Lite, Qwen3-30B-A3B local share, "
                          "fp8 Mixtral)")
     ap.add_argument("--profile-case", default=None,
-                    metavar="NAME:T[:uniform][:w8a8] | prologue:T:H:E[:f32] | copy",
+                    metavar="NAME:T[:uniform][:w8a8|:w8a16] | prologue:T:H:E[:f32] | copy",
                     help="profiling driver: 12 cache-flushed fused-layer calls of one workload (names as in "
                          "easyinfra_amd.workloads.SHAPES); prints no JSON line")
     ap.add_argument("--traffic-run", action="store_true",
@@ -67,7 +67,78 @@ def parse():
                          "markdown table, no JSON line, and touches no GPU")
     ap.add_argument("--trace-last", type=int, default=20,
                     help="launches per kernel in the steady-state mean of --trace-summary (the bench's --steps)")
+    ap.add_argument("--counter-summary", nargs="+", default=None, metavar="COUNTER_CSV",
+                    help="summarise rocprofv3 --pmc runs (their *_counter_collection.csv, one per pass) of the same "
+                         "program: per kernel, the mean of every counter over its launches, with the clock "
+                         "(GRBM_GUI_ACTIVE / 8 XCDs / duration), MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / "
+                         "cycles) and FETCH_SIZE / WRITE_SIZE in MB scaled by --fetch-scale / --write-scale; prints a "
+                         "markdown table, no JSON line, and touches no GPU")
+    ap.add_argument("--fetch-scale", type=float, default=2.0,
+                    help="bytes per FETCH_SIZE KiB unit / 1024 (the counter read for a copy of known size)")
+    ap.add_argument("--write-scale", type=float, default=1.0, help="likewise for WRITE_SIZE")
+    ap.add_argument("--kernel-filter", default="eimoe::", help="kernels whose name contains this (summaries)")
     return ap.parse_args()
+
+
+def counter_summary(paths, fetch_scale, write_scale, name_filter):
+    """Per-kernel means of rocprofv3 counter passes (one CSV per pass; each dispatch's counters
+    summed over the instances the CSV lists)."""
+    import csv
+    sums = {}      # kernel -> counter -> [total, launches]
+    durs = {}      # kernel -> [total ns, launches] of the pass that had GRBM_GUI_ACTIVE (else the first)
+    for path in paths:
+        per = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                k = (int(r["Dispatch_Id"]), r["Kernel_Name"])
+                e = per.setdefault(k, {"_dur": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+                e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        for (_, name), e in per.items():
+            if name_filter not in name:
+                continue
+            ks = sums.setdefault(_kernel_short_name(name), {})
+            for c, v in e.items():
+                if c == "_dur":
+                    continue
+                t = ks.setdefault(c, [0.0, 0])
+                t[0] += v
+                t[1] += 1
+            if "GRBM_GUI_ACTIVE" in e or _kernel_short_name(name) not in durs:
+                d = durs.setdefault(_kernel_short_name(name), [0.0, 0, "GRBM_GUI_ACTIVE" in e])
+                if "GRBM_GUI_ACTIVE" in e and not d[2]:
+                    d[:] = [0.0, 0, True]
+                d[0] += e["_dur"]
+                d[1] += 1
+    counters = sorted({c for ks in sums.values() for c in ks})
+    extra = []
+    if "GRBM_GUI_ACTIVE" in counters:
+        extra.append("clock (GHz)")
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in counters and "GRBM_GUI_ACTIVE" in counters:
+        extra.append("MFMA busy")
+    if "FETCH_SIZE" in counters:
+        extra.append("FETCH (MB)")
+    if "WRITE_SIZE" in counters:
+        extra.append("WRITE (MB)")
+    print("| kernel | launches | mean under counters (us) | " + " | ".join(extra + counters) + " |")
+    print("|---|---:|---:|" + "---:|" * (len(extra) + len(counters)))
+    for name in sorted(sums, key=lambda n: -durs.get(n, [0, 1])[0]):
+        ks = sums[name]
+        mean = {c: v[0] / v[1] for c, v in ks.items()}
+        d = durs.get(name, [0.0, 1])
+        dur_ns = d[0] / max(d[1], 1)
+        cells = []
+        if "clock (GHz)" in extra:
+            cells.append(f"{mean.get('GRBM_GUI_ACTIVE', 0) / 8 / dur_ns:.2f}" if dur_ns else "")
+        if "MFMA busy" in extra:
+            cyc = mean.get("GRBM_GUI_ACTIVE", 0) / 8
+            cells.append(f"{100 * mean.get('SQ_VALU_MFMA_BUSY_CYCLES', 0) / 1024 / cyc:.1f} %" if cyc else "")
+        if "FETCH (MB)" in extra:
+            cells.append(f"{mean.get('FETCH_SIZE', 0) * 1024 * fetch_scale / 1e6:.1f}")
+        if "WRITE (MB)" in extra:
+            cells.append(f"{mean.get('WRITE_SIZE', 0) * 1024 * write_scale / 1e6:.1f}")
+        cells += [f"{mean[c]:.4g}" if c in mean else "" for c in counters]
+        short = name if len(name) <= 100 else name[:97] + "..."
+        print(f"| `{short}` | {d[1]} | {dur_ns / 1e3:.1f} | " + " | ".join(cells) + " |")
 
 
 def _kernel_short_name(name):
@@ -415,7 +486,7 @@ def profile_case(torch, ops, spec):
     inp = make_inputs(shape, T, device="cuda", uniform_twin="uniform" in parts[2:])
     wgu, wd, scales = inp.w_gate_up, inp.w_down, None   # the workload's own dtype (fp32: the fp32 layer)
     w8a8 = "w8a8" in parts[2:]
-    if w8a8:
+    if w8a8 or "w8a16" in parts[2:]:   # e4m3 weights (per-channel scales), activations e4m3 too for w8a8
         qgu, sgu = ops.quantize_weights_fp8(wgu)
         qd, sd = ops.quantize_weights_fp8(wd)
         wgu, wd, scales = qgu, qd, (sgu, sd)
@@ -433,6 +504,9 @@ def main():
     args = parse()
     if args.trace_summary:
         trace_summary(args.trace_summary, args.trace_last)
+        return
+    if args.counter_summary:
+        counter_summary(args.counter_summary, args.fetch_scale, args.write_scale, args.kernel_filter)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the MoE expert path is built and measured on a single "
