@@ -189,8 +189,8 @@ def test_fused_down_split_query():
 
 
 def test_static_scratch_limit_matches_the_documented_token_count():
-    """The header and INTEGRATION.md give the largest Mixtral-8x7B layer (H 4096, I 14336, 8 experts,
-    top-2) the 64 MiB static scratch holds: 545 tokens with bf16 or fp32 output."""
+    """The largest Mixtral-8x7B layer (H 4096, I 14336, 8 experts, top-2) the 64 MiB static scratch
+    holds, as the header states it: 545 tokens with bf16 or fp32 output."""
     L = _lib.lib()
     cap = L.eimoe_fused_moe_static_bytes()
     assert cap == 64 << 20
