@@ -109,8 +109,10 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
   q.K = I;
   q.k_split = 1;
   q.nb_rows = H;
-  const int tile = gemm_pick_tile(q, kEpiStoreF32, w8a8);
-  if (tile == kTileXS) {
+  // the tile the launch will take (the W8A16 layer is costed as bf16: its workspace query does not
+  // see the weight type; any split chosen here is valid for it, at worst on its LDS tiles)
+  const int tile = gemm_choose_tile(q, kEpiStoreF32, w8a8, w8a8);
+  if (tile == kTileStream) {
     // Few rows per segment: the weight-streaming kernel runs one workgroup per (segment,
     // column group, 32-row chunk, split).  Split until there are about 6 workgroups per CU
     // while the split divides the K steps (64 bf16 / 128 e4m3 bytes each) and leaves each

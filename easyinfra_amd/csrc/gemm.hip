@@ -1471,32 +1471,45 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
   return t;
 }
 
+int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
+  const int ops = !b_fp8 ? 0 : a_fp8 ? 1 : 2;   // the streaming kernel's operand mode
+  const bool stream_ok = stream_gemm_supported(p, epi, ops);
+  const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) /
+                     (p.S > 0 ? p.S : 1);
+  const double expert_bytes = static_cast<double>(p.nb_rows) * p.K * p.k_split * (b_fp8 ? 1 : 2);
+  int tile;
+  if (ops == 2) {
+    // W8A16: the LDS tiles widen the e4m3 weights through registers, the streaming kernel in
+    // registers on the way to the MFMA.  Measured (cold, one box; Mixtral-8x7B 1-64 tokens):
+    // streaming gate/up 49-211 us against 71-207 on 32x128, the down projection (K split 2)
+    // 30-105 against 99-123; 128x128 from 32 expected rows per segment (128 tokens: gate/up 271
+    // vs 307 streamed, down 134 vs 164); the Qwen3-30B-A3B share streams at 32 and 256 tokens
+    // (gate/up 24 / 34 us against 37 / 38 on 32x128).
+    tile = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    if (tile == kTileL && (static_cast<long long>(p.max_rows) / 256 + p.S) * (p.N / gemm_out_cols_per_tile(kTileL, epi)) *
+                                  p.k_split < kNumCu)
+      tile = kTileM;
+    while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) ++tile;
+  } else {
+    tile = gemm_pick_tile(p, epi, b_fp8);
+  }
+  // a few rows per segment: stream the weights instead of tiling them through LDS, except W8A8 on
+  // experts too large for the caches, whose LDS tiles read the weights non-temporally: from two
+  // expected rows per expert the 16x64 tile beat streaming (Mixtral-8x7B 8 / 16 tokens, cold: gate/up
+  // 113 / 160 us against 131 / 170, down 58 / 73 against 65 / 84; the layers 0.208 / 0.279 ->
+  // 0.184-0.194 / 0.260 ms); 1 and 2 tokens stream (their layers 7 and 31 us slower on the LDS
+  // tiles), 4 tokens measured either way by 10 % on two boxes.
+  const bool w8a8_lds = ops == 1 && expert_bytes >= 32.0 * 1024 * 1024 && avg >= 2.0;
+  if (tile == kTileXS && stream_ok && !w8a8_lds) tile = kTileStream;
+  return tile;
+}
+
 hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8, int max_rows, int tile,
                                hipStream_t s) {
   if (a_fp8 && !b_fp8) return hipErrorInvalidValue;
   const int ops = !b_fp8 ? 0 : a_fp8 ? 1 : 2;   // the streaming kernel's operand mode
   const bool stream_ok = stream_gemm_supported(p, epi, ops);
-  if (tile == kTileAuto) {
-    if (ops == 2) {
-      // W8A16: the LDS tiles widen the e4m3 weights through registers, the streaming kernel in
-      // registers on the way to the MFMA.  Measured (cold, one box; Mixtral-8x7B 1-64 tokens):
-      // streaming gate/up 49-211 us against 71-207 on 32x128, the down projection (K split 2)
-      // 30-105 against 99-123; 128x128 from 32 expected rows per segment (128 tokens: gate/up 271
-      // vs 307 streamed, down 134 vs 164); the Qwen3-30B-A3B share streams at 32 and 256 tokens
-      // (gate/up 24 / 34 us against 37 / 38 on 32x128).
-      const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) /
-                         (p.S > 0 ? p.S : 1);
-      tile = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
-      if (tile == kTileL && (static_cast<long long>(p.max_rows) / 256 + p.S) * (p.N / gemm_out_cols_per_tile(kTileL, epi)) *
-                                    p.k_split < kNumCu)
-        tile = kTileM;
-      while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) ++tile;
-    } else {
-      tile = gemm_pick_tile(p, epi, b_fp8);
-    }
-    // a few rows per segment: stream the weights instead of tiling them through LDS
-    if (tile == kTileXS && stream_ok) tile = kTileStream;
-  }
+  if (tile == kTileAuto) tile = gemm_choose_tile(p, epi, b_fp8, a_fp8);
   if (tile == kTileStream) {
     if (!stream_ok) return hipErrorInvalidValue;
     const double avg = static_cast<double>(max_rows) / (p.S > 0 ? p.S : 1);

@@ -123,6 +123,9 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
 // Tile for a launch: from the expected rows per segment, the output width and the bytes of
 // one expert's weights (rows_hint/max_rows, p.S, p.N, p.K * p.k_split, nb_rows).
 int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8);
+// The tile an automatic launch takes (kTileStream included): gemm_pick_tile's choice, the W8A16
+// rule, and the switch to the weight-streaming kernel where it applies.
+int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8);
 // Weight-streaming kernel (stream.hip) for segments of a few rows.  ops: 0 bf16 x bf16, 1 e4m3 x
 // e4m3 (W8A8, with p.a_scale / p.b_scale), 2 e4m3 weights x bf16 activations (W8A16, p.b_scale).
 bool stream_gemm_supported(const GemmArgs& p, int epi, int ops);
