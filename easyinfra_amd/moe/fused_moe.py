@@ -55,8 +55,10 @@ class HipFusedMoE(nn.Module):
         if activation_key != "silu":
             raise NotImplementedError(f"activation {activation_key!r}: the fused epilogue implements SiLU*mul only")
         if gate_up_bias or down_bias:
-            # fused_moe_kernel accepts bias pointers but never reads them (fused_moe.py:213-296);
-            # refuse rather than silently ignore.
+            # The reference's fused path cannot run with a bias either: its launcher evaluates
+            # `bias.stride(0) if bias else 0` (fused_moe.py:362), the truth value of an [E, N]
+            # tensor, which torch refuses with a RuntimeError, and fused_moe_kernel takes the bias
+            # pointer without reading it (fused_moe.py:213-296).  Refuse at construction instead.
             raise NotImplementedError("expert biases are not supported by the fused expert path")
         self.activation_key = activation_key
         self.hidden_size = hidden_size

@@ -41,6 +41,13 @@ def test_constructor_checks_mirror_reference():
         HipFusedMoE(0, 64, 128, "relu", False, False, 8, SingleRankGroup(), SingleRankGroup(), phy)
     with pytest.raises(NotImplementedError):
         HipFusedMoE(0, 64, 128, "silu", True, False, 8, SingleRankGroup(), SingleRankGroup(), phy)
+    with pytest.raises(NotImplementedError):
+        HipFusedMoE(0, 64, 128, "silu", False, True, 8, SingleRankGroup(), SingleRankGroup(), phy)
+    # the reference's launcher takes `bias.stride(0) if bias else 0` (fused_moe.py:362): torch
+    # refuses the truth value of a bias tensor, so its fused path raises with a bias as well
+    bias = torch.zeros(8, 256)
+    with pytest.raises(RuntimeError, match="ambiguous"):
+        _ = bias.stride(0) if bias else 0
     ep = HipFusedMoE(0, 64, 128, "silu", False, False, 8, _Group(2, 1), SingleRankGroup(),
                      torch.arange(8).view(2, 4))
     assert ep.num_physical_experts == 4 and ep.forward == ep.forward_ep
