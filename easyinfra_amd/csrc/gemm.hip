@@ -219,16 +219,23 @@ struct Geo {
   static constexpr int MB = WM / 16;
   static constexpr int NB = WN / 16;
   static constexpr bool SILU = epi_silu(EPI);
-  static constexpr int NI = SILU ? NB / 2 : NB;   // adjacent output columns per lane
+  static constexpr int NI = SILU ? NB / 2 : NB;   // output columns per lane
   static constexpr int OUT_BN = SILU ? BN / 2 : BN;
+  // A lane's NI columns come in runs of CH adjacent columns, run g of lane column c starting at
+  // column g*16*CH + c*CH of the wave's block.  One run (CH = NI) but for fp32 outputs of 8
+  // columns per lane, which take runs of 4: each 16-byte store then writes 256 contiguous bytes
+  // of a row across the 16 lane columns, where one run of 8 left every store instruction's row
+  // half-written, in 16-byte pieces 32 bytes apart.
+  static constexpr int CH = (EPI == kEpiStoreF32 && !SILU && NI % 4 == 0) ? 4 : NI;
+  static __device__ __forceinline__ int col_in_run(int j) { return (j / CH) * 16 * CH + j % CH; }
   static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile");
   static_assert(!SILU || (NB % 2 == 0), "silu pairs gate/up fragments");
 
   // B is stored in fragment order: LDS row L = wn*WN + j*16 + c feeds fragment j of wave
   // column wn at lane column c, so the 16 lanes of a fragment read 16 consecutive rows.
-  // Lane column c of fragment j produces output column c*NI + (j % NI) of the wave's
-  // block (NI adjacent columns per lane); in the SiLU tile, fragments j < NI are gate
-  // rows and j >= NI the matching up rows.  Returns the weight row (within the expert).
+  // Lane column c of fragment j produces output column c*CH + col_in_run(j % NI) of the
+  // wave's block; in the SiLU tile, fragments j < NI are gate rows and j >= NI the matching
+  // up rows.  Returns the weight row (within the expert).
   static __device__ __forceinline__ int weight_row_of_lds(int L, int n_tile, int up_off) {
     const int wn = L / WN;
     const int j = (L % WN) >> 4;
@@ -237,7 +244,7 @@ struct Geo {
       const int col = n_tile * (BN / 2) + wn * (WN / 2) + c * NI + (j % NI);
       return j < NI ? col : up_off + col;
     } else {
-      return n_tile * BN + wn * WN + c * NI + j;
+      return n_tile * BN + wn * WN + c * CH + col_in_run(j);
     }
   }
 };
@@ -325,7 +332,7 @@ struct EpiScales {
 template <class G, int MBE>
 __device__ __forceinline__ int epi_col0(const TileCoord& tc, int wn, int lane) {
   return G::SILU ? tc.n_tile * G::OUT_BN + wn * (G::WN / 2) + (lane & 15) * G::NI
-                 : tc.n_tile * G::OUT_BN + wn * G::WN + (lane & 15) * G::NI;
+                 : tc.n_tile * G::OUT_BN + wn * G::WN + (lane & 15) * G::CH;
 }
 
 // Two steps, so that a caller can put other loads between them: the weight scales and the
@@ -346,7 +353,7 @@ __device__ __forceinline__ void epi_load_scales_1(const GemmArgs& p, const TileC
   if (scale) {
 #pragma unroll
     for (int j = 0; j < G::NI; ++j) {
-      sc.cs[j] = scale[col0 + j];
+      sc.cs[j] = scale[col0 + G::col_in_run(j)];
       if constexpr (G::SILU) sc.cs_up[j] = scale[p.up_off + col0 + j];
     }
   } else {
@@ -425,8 +432,13 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const TileCoord& tc,
         for (int j = 0; j < G::NI; ++j) v[j] = acc[i][j][r] * rs[i][r] * cs[j];
         const long long off =
             static_cast<long long>(tc.split) * p.c_split_stride + static_cast<long long>(row) * p.ldc + col0;
-        if constexpr (EPI == kEpiStoreF32) store_f32<G::NI>(static_cast<float*>(p.c) + off, v);
-        else store_bf16<G::NI>(static_cast<uint16_t*>(p.c) + off, v);
+        if constexpr (EPI == kEpiStoreF32) {
+#pragma unroll
+          for (int g = 0; g < G::NI / G::CH; ++g)
+            store_f32<G::CH>(static_cast<float*>(p.c) + off + g * 16 * G::CH, v + g * G::CH);
+        } else {
+          store_bf16<G::NI>(static_cast<uint16_t*>(p.c) + off, v);
+        }
       }
     }
   }
