@@ -313,11 +313,12 @@ int eimoe_release_streams(void) {
     AuxStream& a = g_aux[dev];
     if (!a.stream && !a.fork && !a.join) continue;
     int r = hip_check(hipSetDevice(dev), "set device");
-    // the stream's work (shared experts of a layer still running) ends before it is destroyed
+    // the stream's work (shared experts of a layer still running) ends before it is destroyed;
+    // each handle is cleared once destroyed, so a call after a failure here releases only the rest
     if (!r && a.stream) r = hip_check(hipStreamSynchronize(a.stream), "aux stream synchronize");
-    if (!r && a.stream) r = hip_check(hipStreamDestroy(a.stream), "aux stream destroy");
-    if (!r && a.fork) r = hip_check(hipEventDestroy(a.fork), "fork event destroy");
-    if (!r && a.join) r = hip_check(hipEventDestroy(a.join), "join event destroy");
+    if (!r && a.stream && !(r = hip_check(hipStreamDestroy(a.stream), "aux stream destroy"))) a.stream = nullptr;
+    if (!r && a.fork && !(r = hip_check(hipEventDestroy(a.fork), "fork event destroy"))) a.fork = nullptr;
+    if (!r && a.join && !(r = hip_check(hipEventDestroy(a.join), "join event destroy"))) a.join = nullptr;
     if (r) {
       hipSetDevice(prev);
       return r;
