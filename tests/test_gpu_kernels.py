@@ -682,6 +682,37 @@ def test_fp8_weight_pingpong_gemms(dev, H, I, k_split):
             torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
 
 
+# W8A16 launches of more than 64 segments leave the persistent ping-pong kernel (its schedule holds
+# one segment per lane) for the lock-step 256x256 kernel that widens the e4m3 weights through
+# registers: 70 segments with empty ones and every remainder height, against the oracle's e4m3 GEMMs.
+def test_fp8_weight_256_tile_beyond_64_segments(dev):
+    g = torch.Generator().manual_seed(1070)
+    H, I = 256, 256
+    counts = torch.randint(0, 300, (70,), generator=g).tolist()
+    counts[3], counts[40], counts[69] = 0, 64, 257
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 400
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
+    wgu = torch.randn(E, 2 * I, H, generator=g) * 0.02
+    wd = torch.randn(E, H, I, generator=g) * 0.02
+    qgu, sgu = oracle.quantize_weights_fp8(wgu)
+    qd, sd = oracle.quantize_weights_fp8(wd)
+    hs = (torch.randn(rows, I, generator=g) * 0.5).to(torch.bfloat16)
+    h = cpu(ops.gemm_gate_up_silu(x.to(dev), qgu.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev),
+                                  w_scale=sgu.to(dev), tile=1)).float()
+    y = cpu(ops.gemm_down(hs.to(dev), qd.to(dev), off_t.to(dev), rows, w_scale=sd.to(dev), tile=1)).sum(0)
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        gu = (x[a_rows[a:b].long()].float() @ qgu[e].float().T) * sgu[e]
+        torch.testing.assert_close(h[a:b], oracle.silu(gu[:, :I]) * gu[:, I:], rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(y[a:b], (hs[a:b].float() @ qd[e].float().T) * sd[e], rtol=1e-3, atol=1e-3)
+
+
 # Segment remainders of every height class: a segment's last tile is a quarter, half or full
 # tile (256x256: 64 / 128 / 256 rows; 128x128: 32 / 64 / 128), and the last m-tile group of a
 # long segment takes the leftover tiles (10 m-tiles of 256 rows: groups of 4 and 6).
