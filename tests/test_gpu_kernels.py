@@ -682,14 +682,17 @@ def test_fp8_weight_pingpong_gemms(dev, H, I, k_split):
             torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
 
 
-# W8A16 launches of more than 64 segments leave the persistent ping-pong kernel (its schedule holds
-# one segment per lane) for the lock-step 256x256 kernel that widens the e4m3 weights through
-# registers: 70 segments with empty ones and every remainder height, against the oracle's e4m3 GEMMs.
-def test_fp8_weight_256_tile_beyond_64_segments(dev):
-    g = torch.Generator().manual_seed(1070)
-    H, I = 256, 256
-    counts = torch.randint(0, 300, (70,), generator=g).tolist()
-    counts[3], counts[40], counts[69] = 0, 64, 257
+# W8A16 launches that the persistent ping-pong kernel does not take (more than 64 segments: its
+# schedule holds one segment per lane; K not a multiple of its 128-k weight stage) run the
+# lock-step 256x256 kernel that widens the e4m3 weights through registers: 70 segments with empty
+# ones and every remainder height, and K = 192 on 7 segments, against the oracle's e4m3 GEMMs (the
+# down projection where its 256-column tile divides H).
+@pytest.mark.parametrize("n_seg,H", [(70, 256), (7, 192)])
+def test_fp8_weight_256_tile_lockstep_fallback(dev, n_seg, H):
+    g = torch.Generator().manual_seed(1000 + n_seg + H)
+    I = 256
+    counts = torch.randint(0, 300, (n_seg,), generator=g).tolist()
+    counts[3], counts[-3], counts[-1] = 0, 64, 257
     E = len(counts)
     off, off_t = _segments(counts)
     rows = int(off[-1])
@@ -703,14 +706,18 @@ def test_fp8_weight_256_tile_beyond_64_segments(dev):
     hs = (torch.randn(rows, I, generator=g) * 0.5).to(torch.bfloat16)
     h = cpu(ops.gemm_gate_up_silu(x.to(dev), qgu.to(dev), off_t.to(dev), rows, a_rows=a_rows.to(dev),
                                   w_scale=sgu.to(dev), tile=1)).float()
-    y = cpu(ops.gemm_down(hs.to(dev), qd.to(dev), off_t.to(dev), rows, w_scale=sd.to(dev), tile=1)).sum(0)
+    down = H % 256 == 0
+    if down:
+        y = cpu(ops.gemm_down(hs.to(dev), qd.to(dev), off_t.to(dev), rows, w_scale=sd.to(dev), tile=1)).sum(0)
     for e in range(E):
         a, b = int(off[e]), int(off[e + 1])
         if b == a:
             continue
         gu = (x[a_rows[a:b].long()].float() @ qgu[e].float().T) * sgu[e]
         torch.testing.assert_close(h[a:b], oracle.silu(gu[:, :I]) * gu[:, I:], rtol=1e-2, atol=1e-2)
-        torch.testing.assert_close(y[a:b], (hs[a:b].float() @ qd[e].float().T) * sd[e], rtol=1e-3, atol=1e-3)
+        if down:
+            yref = (hs[a:b].float() @ qd[e].float().T) * sd[e]
+            torch.testing.assert_close(y[a:b], yref, rtol=1e-3, atol=1e-3)
 
 
 # Segment remainders of every height class: a segment's last tile is a quarter, half or full
