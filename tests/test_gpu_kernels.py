@@ -584,10 +584,13 @@ def test_quantize_rows_fp8_bit_exact(dev, shape, dtype):
     assert torch.equal(cpu(q).reshape(-1, shape[-1]).view(torch.uint8), rq.view(torch.uint8))
 
 
-@pytest.mark.parametrize("tile", [2, 4])
-def test_fp8_weight_gemms(dev, tile):
-    g = torch.Generator().manual_seed(tile)
-    H, I, counts = 256, 256, [20, 0, 70]
+# W8A16 on the LDS tiles that widen e4m3 weights through registers; the small counts put each
+# segment in one m-tile, so the weight DMA carries the non-temporal hint.
+@pytest.mark.parametrize("tile,counts", [(2, [20, 0, 70]), (3, [20, 0, 70]), (4, [20, 0, 70]), (2, [5, 0, 12]),
+                                         (3, [5, 0, 12]), (4, [5, 0, 12])])
+def test_fp8_weight_gemms(dev, tile, counts):
+    g = torch.Generator().manual_seed(tile + len(counts) * counts[0])
+    H, I = 256, 256
     E = len(counts)
     off, off_t = _segments(counts)
     rows = int(off[-1])
