@@ -112,10 +112,12 @@ def test_w8a16_layer_meets_fp8_tolerance(dev):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("T", [64, 8192])
+@pytest.mark.parametrize("T", [1, 8, 64, 8192])
 def test_fp8_mixtral_real_shape(dev, T):
     """Mixtral-8x7B with fp8-e4m3 weights (per-channel absmax/448), every row, against the bf16
-    fp32 reference and against the oracle's own fp8 forward of the same mode."""
+    fp32 reference and against the oracle's own fp8 forward of the same mode (1 token: the
+    streaming kernels; 8: W8A8 on the 16x64 tiles with non-temporal weight DMA; 64 and 8192: the
+    32x128 and 256x256 tiles)."""
     import json
     inp = make_inputs(SHAPES["mixtral-8x7b-fp8"], T, device=dev)
     qgu, sgu = ops.quantize_weights_fp8(inp.w_gate_up)
