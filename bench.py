@@ -16,8 +16,9 @@ Prints ONE JSON line.  Besides the contract fields it carries:
   layer / decode / kernels_ms   whole-layer TFLOP/s, the 64-token decode batch
                 (HBM-bound) and the per-kernel breakdown
   suite         the other workloads, warm and cache-cold: tiny fp32, DeepSeek-V2-Lite
-                (zipf + uniform twin, and routed by the DeepSeek-V3 gate), the DeepSeek-V3
-                gate alone, the Qwen3 local share at 1..2048 tokens, fp8 Mixtral (W8A8 and W8A16)
+                (4096 and 768 tokens, zipf + uniform twin, and routed by the DeepSeek-V3
+                gate), the DeepSeek-V3 gate alone, the Qwen3 local share at 1..2048 tokens,
+                fp8 Mixtral (W8A8 and W8A16)
 """
 from __future__ import annotations
 
@@ -422,6 +423,13 @@ def suite(torch, ops, mix_inp, steps, warmup):
                      torch, ops, steps, warmup, flush)
     skew["skew_over_uniform"] = round(skew["ms"] / uni["ms"], 3)
     out += [skew, uni]
+    # a mid-size batch (72 rows per expert on average): the routed GEMMs on other tiles
+    mid = layer_case("deepseek-v2-lite T=768 zipf(1.2) + 2 shared", make_inputs(ds, 768, device=dev), torch, ops,
+                     steps, warmup, flush)
+    mid_u = layer_case("deepseek-v2-lite T=768 uniform twin", make_inputs(ds, 768, device=dev, uniform_twin=True),
+                       torch, ops, steps, warmup, flush)
+    mid["skew_over_uniform"] = round(mid["ms"] / mid_u["ms"], 3)
+    out += [mid, mid_u]
     # the DeepSeek-V3 gate (sigmoid, correction bias, 8 groups keep 4, scaling 2.5) routing the
     # same layer, and the gate alone at DeepSeek-V3's own size (4096 tokens, 256 experts, top-8)
     ds_inp = make_inputs(ds, 4096, device=dev)
@@ -435,7 +443,7 @@ def suite(torch, ops, mix_inp, steps, warmup):
     out.append(prologue_case(torch, ops, steps, warmup, flush, 8192, 4096, 8, True, "Mixtral-8x7B"))
     out.append(prologue_case(torch, ops, steps, warmup, flush, 4096, 7168, 256, False, "DeepSeek-V3"))
     qw = SHAPES["qwen3-30b-a3b-local32"]
-    for T in (1, 32, 256, 2048):
+    for T in (1, 32, 256, 768, 2048):
         hot = layer_case(f"qwen3-30b-a3b local 32/128 T={T} hot:cold 8:1", make_inputs(qw, T, device=dev), torch, ops,
                          steps, warmup, flush)
         twin = layer_case(f"qwen3-30b-a3b local 32/128 T={T} uniform twin",

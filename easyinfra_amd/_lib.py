@@ -16,7 +16,7 @@ ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_WORKSPACE, ERR_HIP = -1, -2, -3, 
 F32, BF16, FP8 = 0, 1, 2
 RENORMALIZE, Y_F32, W8A8, ROUTING_IN, H_SPLIT, FP32 = 1, 2, 4, 8, 16, 32
 LOGITS_BF16 = 1   # eimoe_moe_prologue flag
-TILE_AUTO, TILE_256x256, TILE_128x128, TILE_32x128, TILE_16x64, TILE_STREAM = 0, 1, 2, 3, 4, 5
+TILE_AUTO, TILE_256x256, TILE_128x128, TILE_32x128, TILE_16x64, TILE_STREAM, TILE_64x128 = 0, 1, 2, 3, 4, 5, 6
 MAX_TOPK, MAX_EXPERTS, MAX_SEGMENTS = 32, 512, 1024
 
 _i32p = POINTER(ctypes.c_int32)

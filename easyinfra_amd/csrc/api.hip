@@ -86,7 +86,7 @@ int check_gemm_common(int max_rows, int n_seg, int e_mod) {
 }
 
 int check_tile(int tile, int epi, int N) {
-  if (tile < EIMOE_TILE_AUTO || tile > EIMOE_TILE_STREAM) return fail(EIMOE_ERR_SHAPE, "tile=%d unknown", tile);
+  if (tile < EIMOE_TILE_AUTO || tile > EIMOE_TILE_64x128) return fail(EIMOE_ERR_SHAPE, "tile=%d unknown", tile);
   if (tile != EIMOE_TILE_AUTO) {
     const int oc = gemm_out_cols_per_tile(tile, epi);
     if (N % oc != 0) return fail(EIMOE_ERR_ALIGN, "N=%d not a multiple of the tile's %d output columns", N, oc);
@@ -133,7 +133,7 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
   if (expert_bytes >= 32.0 * 1024 * 1024 && tile != kTileL)
     return (I / (w8a8 ? 128 : 64)) % 2 == 0 ? 2 : 1;
   if (w8a8) I /= 2;   // e4m3 tiles run at twice the bf16 rate: cost them as half the K
-  const int bm = tile == kTileL ? 256 : tile == kTileM ? 128 : tile == kTileS ? 32 : 16;
+  const int bm = tile == kTileL ? 256 : tile == kTileM ? 128 : tile == kTileMS ? 64 : tile == kTileS ? 32 : 16;
   const int bn = gemm_out_cols_per_tile(tile, kEpiStoreF32);
   const int rows = rows_hint > 0 ? std::min(rows_hint, max_rows) : max_rows;
   // m-tiles in full-tile units from the expected rows per segment: whole tiles plus the remainder's

@@ -1420,6 +1420,7 @@ static hipError_t launch_epi(const GemmArgs& p, int max_rows, int tile, bool a_f
         return launch_pp<EPI, 0>(p, max_rows, s);
       }
     case kTileM: return launch_cfg<128, 128, 2, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
+    case kTileMS: return launch_cfg<64, 128, 2, 2, EPI, BFP8, 4>(p, max_rows, a_fp8, s);
     case kTileS: return launch_cfg<32, 128, 1, 4, EPI, BFP8, 1>(p, max_rows, a_fp8, s);
     case kTileXS: return launch_cfg<16, 64, 1, 2, EPI, BFP8, 1>(p, max_rows, a_fp8, s);
     default: return hipErrorInvalidValue;
@@ -1432,6 +1433,7 @@ int gemm_out_cols_per_tile(int tile, int epi) {
   switch (tile) {
     case kTileL: bn = 256; break;
     case kTileM: bn = 128; break;
+    case kTileMS: bn = 128; break;
     case kTileS: bn = 128; break;
     case kTileXS: bn = 64; break;
     default: return 0;
@@ -1452,6 +1454,38 @@ int gemm_out_cols_per_tile(int tile, int epi) {
 //    us skewed, 580 vs 657 uniform against 128x128); the down projection (short K) wants
 //    more, smaller tiles: 128x128 below ~384 expected rows per segment (Qwen3 2048 tokens:
 //    46 vs 62 us), 32x128 below ~96.
+// Routed launches (8 or more segments) of bf16 experts that stay in cache, from 8 to a few
+// hundred expected rows per segment.  What decides is whether a tile shape spreads the weight
+// panels over all CUs: the 256x256 tile is the fastest per tile (persistent, ping-pong) but with
+// few experts and narrow outputs it leaves CUs idle, the 64x128 tile (three workgroups per CU,
+// one m-tile for most segments) covers the CUs where 128x128 makes too few tiles and 32x128 reads
+// each weight panel once per 32 rows.  Tile counts are estimated at the expected rows.  Measured
+// per GEMM, single launches on the routed segments (cold, one box; us):
+//  * Qwen3-30B-A3B 32-expert share, 768 tokens (46 rows per expert, 198 at most): gate/up 52.8 on
+//    64x128 against 63.2 / 63.7 / 62.7 on 128x128 / 32x128 / 256x256, down 35.9 against 49.1 /
+//    48.2 / 41.4; 256 tokens (15 rows): gate/up 51.0 on 32x128 (64x128 52.9, 128x128 54.4), down
+//    33.4 on 128x128 (32x128 34.9);
+//  * DeepSeek-V2-Lite, 768 tokens (72 rows, zipf routing): gate/up 152.9 on 256x256 against
+//    174.3 / 178.6 / 218.9 on 64x128 / 128x128 / 32x128, down 88.2 against 99.5 / 105.1 / 115.3
+//    (uniform routing: 168.7 and 87.2 on 256x256); 128 tokens (12 rows): gate/up 112.6 on 128x128
+//    against 125.3 streamed and 128.4 on 32x128.
+static int routed_small_gate_up_tile(const GemmArgs& p, int S, double avg, int t) {
+  const long long tiles_l = static_cast<long long>(S) * static_cast<long long>((avg + 255) / 256) * (p.N / 128);
+  const long long tiles_m = static_cast<long long>(S) * static_cast<long long>((avg + 127) / 128) * (p.N / 64);
+  if (avg >= 40 && tiles_l >= kNumCu) return kTileL;
+  if (avg >= 20 && avg < 64) return kTileMS;
+  if (avg >= 8 && avg < 20 && tiles_m >= 2 * kNumCu) return kTileM;
+  return t;
+}
+
+static int routed_small_down_tile(const GemmArgs& p, int S, double avg) {
+  const long long tiles_ms = static_cast<long long>(S) * static_cast<long long>((avg + 63) / 64) * (p.N / 128);
+  const long long tiles_l = static_cast<long long>(S) * static_cast<long long>((avg + 255) / 256) * (p.N / 256);
+  if (avg >= 20 && avg < 64 && tiles_ms <= 3 * kNumCu) return kTileMS;   // one round of 64x128 workgroups
+  if (avg >= 36 && tiles_l >= 2 * kNumCu) return kTileL;
+  return kTileM;
+}
+
 int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
   const int S = p.S > 0 ? p.S : 1;
   const double avg_bound = static_cast<double>(p.max_rows) / S;
@@ -1470,8 +1504,10 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
     // tokens (~3900 local rows, 56-551 per expert) measured 72 us on 256x256 tiles and 89 us on
     // 128x128 (the expected 125 rows per expert would pick the latter).
     t = avg_bound >= 256 ? kTileL : avg_bound >= 96 ? kTileM : avg_bound >= 24 ? kTileS : kTileXS;
+    if (!b_fp8 && S >= 8 && avg_bound < 256) t = routed_small_gate_up_tile(p, S, avg, t);
   } else {
     t = avg < 6 ? kTileXS : avg < 96 ? kTileS : avg < 384 ? kTileM : kTileL;
+    if (!b_fp8 && S >= 8 && avg >= 8 && avg < 384) t = routed_small_down_tile(p, S, avg);
   }
   if (t == kTileL) {
     // fewer 256x256 tiles than CUs (a dense shared-expert launch, say) leaves CUs idle: step down
@@ -1479,7 +1515,7 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
     const int oc = gemm_out_cols_per_tile(kTileL, epi);
     if (p.N % oc == 0 && mt * (p.N / oc) * p.k_split < kNumCu) t = kTileM;
   }
-  while (t != kTileXS && p.N % gemm_out_cols_per_tile(t, epi) != 0) ++t;
+  while (t != kTileXS && p.N % gemm_out_cols_per_tile(t, epi) != 0) t = tile_step_down(t);
   return t;
 }
 
@@ -1501,7 +1537,7 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
     if (tile == kTileL && (static_cast<long long>(p.max_rows) / 256 + p.S) * (p.N / gemm_out_cols_per_tile(kTileL, epi)) *
                                   p.k_split < kNumCu)
       tile = kTileM;
-    while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) ++tile;
+    while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) tile = tile_step_down(tile);
   } else {
     tile = gemm_pick_tile(p, epi, b_fp8);
   }
@@ -1528,7 +1564,10 @@ hipError_t launch_grouped_gemm(const GemmArgs& p, int epi, bool b_fp8, bool a_fp
     return launch_stream_gemm(p, epi, ops, max_rows, avg > 8 ? 2 : 1, s);
   }
   // Non-temporal weight DMA on the smaller LDS tiles when a segment's expected rows (with half
-  // again for skew) fit one m-tile, so each weight panel is read once (decode batches).
+  // again for skew) fit one m-tile, so each weight panel is read once (decode batches).  Not on
+  // the 64x128 tile, which runs mid-size batches of cache-resident experts (with the hint: the
+  // Qwen3 share at 384 tokens 86.5 -> 94.9 us warm, DeepSeek-V2-Lite at 256 tokens 222 -> 231 us
+  // cold, within noise elsewhere; one box).
   GemmArgs q = p;
   {
     const int bm = tile == kTileM ? 128 : tile == kTileS ? 32 : tile == kTileXS ? 16 : 0;
@@ -1576,11 +1615,12 @@ hipError_t launch_grouped_gemm_f32(const GemmArgs& p, int epi, int max_rows, int
                        (p.S > 0 ? p.S : 1);
     tile = avg >= 32 ? kTileM : avg >= 12 ? kTileS : kTileXS;
   }
-  // No 256x256 or streaming fp32 kernel: those requests take the 128x128 tile.  Whatever the
-  // start, step down until the tile's output columns divide N (the tile's columns are its grid's
-  // only bound on N), and refuse a tile that still does not fit rather than leave columns unwritten.
-  if (tile == kTileL || tile == kTileStream) tile = kTileM;
-  while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) ++tile;
+  // No 256x256, 64x128 or streaming fp32 kernel: those requests take the 128x128 tile.  Whatever
+  // the start, step down until the tile's output columns divide N (the tile's columns are its
+  // grid's only bound on N), and refuse a tile that still does not fit rather than leave columns
+  // unwritten.
+  if (tile == kTileL || tile == kTileMS || tile == kTileStream) tile = kTileM;
+  while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) tile = tile_step_down(tile);
   if (p.N % gemm_out_cols_per_tile(tile, epi) != 0) return hipErrorInvalidValue;
   return epi == kEpiSiluF32 ? launch_epi_f32<kEpiSiluF32>(p, max_rows, tile, s)
                             : launch_epi_f32<kEpiStoreF32>(p, max_rows, tile, s);

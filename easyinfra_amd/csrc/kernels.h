@@ -43,7 +43,10 @@ struct GemmArgs {
 };
 
 // Tile shape selector; the launcher maps it to a kernel instantiation.
-enum TileCfg : int { kTileAuto = 0, kTileL = 1, kTileM = 2, kTileS = 3, kTileXS = 4, kTileStream = 5 };
+enum TileCfg : int { kTileAuto = 0, kTileL = 1, kTileM = 2, kTileS = 3, kTileXS = 4, kTileStream = 5, kTileMS = 6 };
+// The next smaller LDS tile (256x256 -> 128x128 -> 32x128 -> 16x64; 64x128 -> 32x128), for a tile
+// whose output columns do not divide N.
+constexpr int tile_step_down(int t) { return t == kTileMS ? kTileS : t + 1; }
 
 hipError_t launch_router_topk(const float* logits, int T, int E, int k, int renorm, int32_t* ids, float* w,
                               hipStream_t s);

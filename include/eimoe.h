@@ -62,9 +62,10 @@ enum {
  * weight-streaming kernel for a few rows per segment (bf16 weights with K % 64 == 0, or e4m3
  * weights with K % 128 == 0 and bf16 or, in the W8A8 entry points, e4m3 activations; the output
  * columns a multiple of 16 for gate/up, 32 otherwise); automatic selection uses it when the
- * average rows per segment are small. */
+ * average rows per segment are small.  The fp32 layer has no 256x256, 64x128 or streaming
+ * kernel: those requests take the 128x128 tile there. */
 enum { EIMOE_TILE_AUTO = 0, EIMOE_TILE_256x256 = 1, EIMOE_TILE_128x128 = 2, EIMOE_TILE_32x128 = 3,
-       EIMOE_TILE_16x64 = 4, EIMOE_TILE_STREAM = 5 };
+       EIMOE_TILE_16x64 = 4, EIMOE_TILE_STREAM = 5, EIMOE_TILE_64x128 = 6 };
 
 #define EIMOE_MAX_TOPK 32
 #define EIMOE_MAX_EXPERTS 512

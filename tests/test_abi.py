@@ -124,6 +124,11 @@ def test_gemm_validation():
                None) == _lib.ERR_SHAPE
     assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.BF16, None, 128, 64, 1, 1, 1, 4, 1, 9,
                None) == _lib.ERR_SHAPE
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.BF16, None, 128, 64, 1, 1, 1, 4, 1,
+               _lib.TILE_64x128 + 1, None) == _lib.ERR_SHAPE
+    # the 64x128 tile writes 64 gate/up output columns: I = 96 does not fit it
+    assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.BF16, None, 128, 96, 1, 1, 1, 4, 1,
+               _lib.TILE_64x128, None) == _lib.ERR_ALIGN
     # tile whose output width does not divide I
     assert _rc("eimoe_gemm_gate_up_silu", 1, None, 4, 128, 1, _lib.BF16, None, 128, 96, 1, 1, 1, 4, 1,
                _lib.TILE_256x256, None) == _lib.ERR_ALIGN

@@ -339,7 +339,7 @@ def _segments(counts):
     return off, torch.as_tensor(off)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 5, 6])
 @pytest.mark.parametrize("counts", [[0, 5, 300, 1, 64], [17], [0, 0, 3]])
 def test_gate_up_silu(dev, tile, counts):
     g = torch.Generator().manual_seed(sum(counts) + tile)
@@ -391,7 +391,8 @@ def test_gate_up_silu_extreme_gates(dev, tile):
     assert ((h - ref).abs() <= 1e-2 * ref.abs() + 1e-6).all(), (h - ref).abs().max()
 
 
-@pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 4), (5, 1), (5, 2), (5, 8)])
+@pytest.mark.parametrize("tile,k_split", [(1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 4), (5, 1), (5, 2), (5, 8),
+                                          (6, 1), (6, 2)])
 def test_down_gemm(dev, tile, k_split):
     g = torch.Generator().manual_seed(31 + tile * 7 + k_split)
     H, I = 256, 512
@@ -587,7 +588,7 @@ def test_quantize_rows_fp8_bit_exact(dev, shape, dtype):
 # W8A16 on the LDS tiles that widen e4m3 weights through registers; the small counts put each
 # segment in one m-tile, so the weight DMA carries the non-temporal hint.
 @pytest.mark.parametrize("tile,counts", [(2, [20, 0, 70]), (3, [20, 0, 70]), (4, [20, 0, 70]), (2, [5, 0, 12]),
-                                         (3, [5, 0, 12]), (4, [5, 0, 12])])
+                                         (3, [5, 0, 12]), (4, [5, 0, 12]), (6, [20, 0, 70]), (6, [5, 0, 12])])
 def test_fp8_weight_gemms(dev, tile, counts):
     g = torch.Generator().manual_seed(tile + len(counts) * counts[0])
     H, I = 256, 256
@@ -724,13 +725,15 @@ def test_fp8_weight_256_tile_lockstep_fallback(dev, n_seg, H):
 
 
 # Segment remainders of every height class: a segment's last tile is a quarter, half or full
-# tile (256x256: 64 / 128 / 256 rows; 128x128: 32 / 64 / 128), and the last m-tile group of a
-# long segment takes the leftover tiles (10 m-tiles of 256 rows: groups of 4 and 6).
+# tile (256x256: 64 / 128 / 256 rows; 128x128: 32 / 64 / 128; 64x128, whose two wave rows of
+# 32 have no quarter: 32 / 64), and the last m-tile group of a long segment takes the leftover
+# tiles (10 m-tiles of 256 rows: groups of 4 and 6; 12 of 64 rows: groups of 4, 4 and 4).
 REMAINDER_COUNTS = {1: [257, 320, 321, 128, 129, 712, 63, 9 * 256 + 2, 0],
-                    2: [33, 32, 64, 65, 129, 127, 11 * 128 + 7, 0, 1]}
+                    2: [33, 32, 64, 65, 129, 127, 11 * 128 + 7, 0, 1],
+                    6: [33, 32, 64, 65, 97, 127, 11 * 64 + 7, 0, 1, 9 * 64 + 40]}
 
 
-@pytest.mark.parametrize("tile", [1, 2])
+@pytest.mark.parametrize("tile", [1, 2, 6])
 @pytest.mark.parametrize("k_split", [1, 2])
 def test_gemms_remainder_tile_heights(dev, tile, k_split):
     counts = REMAINDER_COUNTS[tile]
@@ -757,7 +760,34 @@ def test_gemms_remainder_tile_heights(dev, tile, k_split):
         torch.testing.assert_close(y[a:b], h[a:b] @ wd[e].float().T, rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("tile", [1, 2])
+# Every LDS tile adds the K slabs of a row in the same order on the same MFMA, so the 64x128,
+# 128x128 and 32x128 tiles (and the 256x256 tile where it divides the output) agree bit for bit
+# on the same segments: gathered rows, remainder heights, empty segments, K split planes.
+@pytest.mark.parametrize("k_split", [1, 2])
+def test_lds_tiles_bit_identical(dev, k_split):
+    counts = [33, 0, 64, 65, 97, 300, 1, 7 * 64 + 5]
+    g = torch.Generator().manual_seed(123 + k_split)
+    H, I = 512, 256
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 200
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32).to(dev)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    wd = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    off_t = off_t.to(dev)
+    hs = {t: cpu(ops.gemm_gate_up_silu(x, wgu, off_t, rows, a_rows=a_rows, tile=t)) for t in (1, 2, 3, 6)}
+    for t in (1, 3, 6):
+        assert torch.equal(hs[t], hs[2]), t
+    h = hs[2].to(dev)
+    ys = {t: cpu(ops.gemm_down(h, wd, off_t, rows, out_dtype=torch.float32, k_split=k_split, tile=t))
+          for t in (1, 2, 3, 6)}
+    for t in (1, 3, 6):
+        assert torch.equal(ys[t], ys[2]), t
+
+
+@pytest.mark.parametrize("tile", [1, 2, 6])
 def test_fp8_gemms_remainder_tile_heights(dev, tile):
     """The same segment layouts on the W8A8 (fp8 x fp8) and W8A16 (fp8 weights) kernels."""
     counts = REMAINDER_COUNTS[tile]
@@ -797,7 +827,7 @@ def test_fp8_gemms_remainder_tile_heights(dev, tile):
 
 # fp32 operands on the fp32 MFMA (the fp32 layer): every LDS tile, remainder heights of the 128x128
 # tile, K split planes; against float64 with only the summation order left to differ.
-@pytest.mark.parametrize("tile", [0, 2, 3, 4])
+@pytest.mark.parametrize("tile", [0, 2, 3, 4, 6])
 @pytest.mark.parametrize("k_split", [1, 2])
 def test_fp32_gemms(dev, tile, k_split):
     counts = [33, 0, 64, 65, 129, 7, 300]

@@ -141,8 +141,9 @@ def test_layer_with_eplb_replicas_matches_logical_layer(dev):
 
 # --------------------------------------------------------------------------- real shapes
 REAL = [("tiny-mixtral-fp32", 512), ("mixtral-8x7b", 1), ("mixtral-8x7b", 8), ("mixtral-8x7b", 64),
-        ("mixtral-8x7b", 8192), ("deepseek-v2-lite", 16), ("deepseek-v2-lite", 4096), ("qwen3-30b-a3b-local32", 1),
-        ("qwen3-30b-a3b-local32", 32), ("qwen3-30b-a3b-local32", 256), ("qwen3-30b-a3b-local32", 2048)]
+        ("mixtral-8x7b", 8192), ("deepseek-v2-lite", 16), ("deepseek-v2-lite", 128), ("deepseek-v2-lite", 768),
+        ("deepseek-v2-lite", 4096), ("qwen3-30b-a3b-local32", 1), ("qwen3-30b-a3b-local32", 32),
+        ("qwen3-30b-a3b-local32", 256), ("qwen3-30b-a3b-local32", 768), ("qwen3-30b-a3b-local32", 2048)]
 
 
 def half_ulp_bf16(t: torch.Tensor) -> torch.Tensor:
