@@ -1441,19 +1441,6 @@ int gemm_out_cols_per_tile(int tile, int epi) {
   return epi_silu(epi) ? bn / 2 : bn;
 }
 
-// Tile heuristic (the host knows only the row bound, or a caller's estimate, and the shapes).
-// Measured on the routed offsets of the workloads (cold caches; us, gate/up + down):
-//  * experts of >= 32 MiB of weights (Mixtral-8x7B) are read from HBM once per row chunk of
-//    a segment, so the tile should cover a segment in one chunk.  64 tokens (16 rows per
-//    expert): bf16 gate/up streams (335 vs 372 with 32x128), the down projection takes
-//    128x128 with K split 2 (159 vs 178 streaming); e4m3 W8A8 takes 32x128 for both (180
-//    vs 190, 84 vs 97).  128-256 tokens (32-64 rows): 128x128 (gate/up 377 and 402 vs 478
-//    and 911 with 32x128).  From 128 rows: 256x256;
-//  * small experts (DeepSeek-V2-Lite, Qwen3 local share) stay in cache: gate/up keeps the
-//    256x256 tile from ~256 rows per segment of the bound (DeepSeek 4096 tokens 717 vs 710
-//    us skewed, 580 vs 657 uniform against 128x128); the down projection (short K) wants
-//    more, smaller tiles: 128x128 below ~384 expected rows per segment (Qwen3 2048 tokens:
-//    46 vs 62 us), 32x128 below ~96.
 // Routed launches (8 or more segments) of bf16 experts that stay in cache, from 8 to a few
 // hundred expected rows per segment.  What decides is whether a tile shape spreads the weight
 // panels over all CUs: the 256x256 tile is the fastest per tile (persistent, ping-pong) but with
@@ -1486,6 +1473,20 @@ static int routed_small_down_tile(const GemmArgs& p, int S, double avg) {
   return kTileM;
 }
 
+// Tile heuristic (the host knows only the row bound, or a caller's estimate, and the shapes).
+// Measured on the routed offsets of the workloads (cold caches; us, gate/up + down):
+//  * experts of >= 32 MiB of weights (Mixtral-8x7B) are read from HBM once per row chunk of
+//    a segment, so the tile should cover a segment in one chunk.  64 tokens (16 rows per
+//    expert): bf16 gate/up streams (335 vs 372 with 32x128), the down projection takes
+//    128x128 with K split 2 (159 vs 178 streaming); e4m3 W8A8 takes 32x128 for both (180
+//    vs 190, 84 vs 97).  128-256 tokens (32-64 rows): 128x128 (gate/up 377 and 402 vs 478
+//    and 911 with 32x128).  From 128 rows: 256x256;
+//  * small experts (DeepSeek-V2-Lite, Qwen3 local share) stay in cache: gate/up keeps the
+//    256x256 tile from ~256 rows per segment of the bound (DeepSeek 4096 tokens 717 vs 710
+//    us skewed, 580 vs 657 uniform against 128x128); the down projection (short K) wants
+//    more, smaller tiles: 128x128 below ~384 expected rows per segment (Qwen3 2048 tokens:
+//    46 vs 62 us), 32x128 below ~96.  Routed bf16 launches of 8 or more segments between 8
+//    and 384 expected rows take routed_small_gate_up_tile / routed_small_down_tile instead.
 int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
   const int S = p.S > 0 ? p.S : 1;
   const double avg_bound = static_cast<double>(p.max_rows) / S;
