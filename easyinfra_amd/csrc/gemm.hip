@@ -1347,6 +1347,132 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8w_kernel(GemmA
   });
 }
 
+// ---------------------------------------------------------------------------- fp8 weights (W8A16), direct-to-LDS
+// The LDS tiles of W8A16 with the e4m3 weight rows DMA'd to LDS as they are (128 k per 128-byte row)
+// and widened to bf16 at the fragment reads, the k assignment of the ping-pong W8A16 tile (within a
+// 64-k activation slab lane group q takes k = 16q + 8*KK + 0..7 in MFMA step KK; one 16-byte weight
+// read per slab covers both steps), so its sums are those of the 256x256 W8A16 tile, bit for bit.
+// A weight chunk serves two activation slabs: its DMA goes out at the top of the odd slab before
+// them, into the stage the chunk before last has left.  Both stages of each operand are distinct
+// objects and the loop is unrolled by four, so every stage index is static.  K % 128 == 0.
+template <class G, int MBE>
+__device__ __forceinline__ void w8a16_slab_mma(f32x4_t (&acc)[MBE][G::NB], const uint16_t* sA, const uint16_t* sB,
+                                               int half, int wm, int wn, int lane) {
+  const int lr = lane & 15;
+  const int q = lane >> 4;
+  const uint8_t* b8 = reinterpret_cast<const uint8_t*>(sB);
+  u32x4_t braw[G::NB];
+#pragma unroll
+  for (int j = 0; j < G::NB; ++j) {
+    const int R = wn * G::WN + j * 16 + lr;
+    braw[j] = *reinterpret_cast<const u32x4_t*>(&b8[R * 128 + (((4 * half + q) ^ swz(R)) << 4)]);
+  }
+#pragma unroll
+  for (int KK = 0; KK < 2; ++KK) {
+    bf16x8_t af[MBE], bw[G::NB];
+#pragma unroll
+    for (int i = 0; i < MBE; ++i) {
+      const int R = wm * 16 * MBE + i * 16 + lr;
+      af[i] = *reinterpret_cast<const bf16x8_t*>(&sA[R * G::BK + (((2 * q + KK) ^ swz(R)) << 3)]);
+    }
+#pragma unroll
+    for (int j = 0; j < G::NB; ++j) bw[j] = widen_fp8x8(braw[j][2 * KK], braw[j][2 * KK + 1]);
+    mma<G, MBE>(acc, af, bw);
+  }
+}
+
+template <int B_PW, int NW>
+__device__ __forceinline__ void issue_b8_dma(const BufRef& b, const uint32_t (&b_voff)[B_PW], uint16_t* sB, int wave,
+                                             int soff, bool b_nt) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto rB = make_rsrc(b.base, b.bytes);
+  if (b_nt) {
+#pragma unroll
+    for (int i = 0; i < B_PW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_void_t*)(sB + (wave * B_PW + i) * 512), 16, b_voff[i], soff,
+                                               0, 2);
+  } else {
+#pragma unroll
+    for (int i = 0; i < B_PW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (lds_void_t*)(sB + (wave * B_PW + i) * 512), 16, b_voff[i], soff,
+                                               0, 0);
+  }
+#endif
+}
+
+template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
+__global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_w8a16_dma_kernel(GemmArgs p) {
+  using G = Geo<BM, BN, WGM, WGN, EPI>;
+  constexpr int BK = G::BK;
+  constexpr int NW = G::NW;
+  constexpr int A_PW = BM / 8 / NW;   // 1 KiB LDS blocks per wave per slab (8 rows each)
+  constexpr int B_PW = BN / 8 / NW;
+  static_assert(A_PW * 8 * NW == BM && B_PW * 8 * NW == BN, "slab split over waves");
+
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * BK];   // BN rows of 128 e4m3 bytes
+  __shared__ __attribute__((aligned(1024))) uint16_t sB1[BN * BK];
+  __shared__ int s_pref[kMaxSeg + 1];
+
+  TileCoord tc;
+  if (!decode_tile<BM, G::OUT_BN, GM>(p, s_pref, tc)) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane >> 3;
+  const long long k0 = static_cast<long long>(tc.split) * p.K;
+
+  const BufRef rA{static_cast<const uint8_t*>(p.a) + k0 * 2, (p.a_rows_cap * p.lda - k0) * 2};
+  uint32_t a_voff[A_PW];
+  a_offsets<A_PW, NW>(p, tc, wave, lane, 2, a_voff);
+  const uint8_t* b_base = expert_weights(p, tc.expert, 1) + k0;
+  const BufRef rB{b_base, p.b_estride - k0};
+  uint32_t b_voff[B_PW];
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i) {
+    const int R = (wave * B_PW + i) * 8 + lrow;
+    const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
+    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb + (((lane & 7) ^ swz(R)) << 4));
+  }
+  const int wm = wave % WGM;
+  const int wn = wave / WGM;
+  const int KT = p.K / BK;   // 64-k activation slabs (even)
+  const int NC = KT / 2;     // 128-k weight chunks
+  const bool nt = p.b_nt != 0;
+  const float* scale = p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows;
+  by_height<BM, G::MB, A_PW>(tc.row_end - tc.row0, [&]<int MBE>() {
+    constexpr int A_CNT = A_PW * MBE / G::MB;
+    f32x4_t acc[MBE][G::NB];
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    issue_a_dma<A_CNT, NW>(rA, a_voff, sA0, wave, 0);
+    issue_b8_dma<B_PW, NW>(rB, b_voff, sB0, wave, 0, nt);
+    __syncthreads();
+    // slab kt + J: activations in SA, its weight chunk in SB (half J % 2 of it); loads the next
+    // slab's activations into SAN and, after an odd slab's issue, the chunk after next into SBN
+    // (clamped near the end: those stages are not read again)
+#define EIMOE_W8_SLAB(J, SA, SAN, SB, SBN)                                                             \
+    if (kt + J < KT) {                                                                               \
+      issue_a_dma<A_CNT, NW>(rA, a_voff, SAN, wave, min(kt + J + 1, KT - 1) * 128);                  \
+      if (J % 2 == 1) issue_b8_dma<B_PW, NW>(rB, b_voff, SBN, wave, min((kt + J + 1) / 2, NC - 1) * 128, nt); \
+      pin_issue();                                                                                   \
+      w8a16_slab_mma<G, MBE>(acc, SA, SB, J % 2, wm, wn, lane);                                       \
+      __syncthreads();                                                                               \
+    }
+    for (int kt = 0; kt < KT; kt += 4) {
+      EIMOE_W8_SLAB(0, sA0, sA1, sB0, sB1)
+      EIMOE_W8_SLAB(1, sA1, sA0, sB0, sB1)
+      EIMOE_W8_SLAB(2, sA0, sA1, sB1, sB0)
+      EIMOE_W8_SLAB(3, sA1, sA0, sB1, sB0)
+    }
+#undef EIMOE_W8_SLAB
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale, nullptr);   // bf16 activations
+  });
+}
+
 // ---------------------------------------------------------------------------- launch
 template <int BM, int BN, int WGM, int WGN, int EPI, bool BFP8, int GM>
 static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStream_t s) {
@@ -1361,9 +1487,19 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
   if (BFP8 && a_fp8)
     hipLaunchKernelGGL((grouped_gemm_fp8_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
-  else if (BFP8)
+  else if (BFP8) {
+    // W8A16: the e4m3 weights DMA'd to LDS and widened at the fragment reads when K allows, else
+    // widened through registers on their way to LDS
+    if constexpr (BM <= 128) {
+      if (p.K % 128 == 0) {
+        hipLaunchKernelGGL((grouped_gemm_w8a16_dma_kernel<BM, BN, WGM, WGN, EPI, GM>),
+                           dim3(static_cast<unsigned>(grid)), dim3(WGM * WGN * 64), 0, s, p);
+        return hipGetLastError();
+      }
+    }
     hipLaunchKernelGGL((grouped_gemm_fp8w_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
+  }
   else
     hipLaunchKernelGGL((grouped_gemm_dma_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
@@ -1528,13 +1664,21 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
   const double expert_bytes = static_cast<double>(p.nb_rows) * p.K * p.k_split * (b_fp8 ? 1 : 2);
   int tile;
   if (ops == 2) {
-    // W8A16: the LDS tiles widen the e4m3 weights through registers, the streaming kernel in
-    // registers on the way to the MFMA.  Measured (cold, one box; Mixtral-8x7B 1-64 tokens):
-    // streaming gate/up 49-211 us against 71-207 on 32x128, the down projection (K split 2)
-    // 30-105 against 99-123; 128x128 from 32 expected rows per segment (128 tokens: gate/up 271
-    // vs 307 streamed, down 134 vs 164); the Qwen3-30B-A3B share streams at 32 and 256 tokens
-    // (gate/up 24 / 34 us against 37 / 38 on 32x128).
-    tile = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    // W8A16: the LDS tiles DMA the e4m3 weights and widen them at the fragment reads, the
+    // streaming kernel widens them in registers on the way to the MFMA.  Experts too large for
+    // the caches, measured on the routed Mixtral-8x7B segments (single GEMMs, cold, one box; us):
+    // gate/up streams below 12 expected rows per segment (32 tokens: 174.9 against 175.0 on
+    // 16x64), then 32x128 (64 tokens: 178.8 against 208.6 streamed), 64x128 from 24 rows (128
+    // tokens: 199.7 against 214.2 on 128x128), 128x128 from 48 (256 tokens: 250.4 against 265.0);
+    // the down projection (K split 2) streams below 12 rows (32 tokens: 88.1 against 93.3 on
+    // 16x64), then 128x128 (64 tokens: 97.9 against 106.7 streamed).  Smaller experts: streaming
+    // below 24 rows (the Qwen3-30B-A3B share at 32 and 256 tokens, gate/up 24 / 34 us against 37 /
+    // 38 on 32x128 with the weights widened through registers), 128x128 from 24.
+    if (expert_bytes >= 32.0 * 1024 * 1024)
+      tile = epi_silu(epi) ? (avg < 12 ? kTileXS : avg < 24 ? kTileS : avg < 48 ? kTileMS : avg < 128 ? kTileM : kTileL)
+                           : (avg < 12 ? kTileXS : avg < 128 ? kTileM : kTileL);
+    else
+      tile = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
     if (tile == kTileL && (static_cast<long long>(p.max_rows) / 256 + p.S) * (p.N / gemm_out_cols_per_tile(kTileL, epi)) *
                                   p.k_split < kNumCu)
       tile = kTileM;

@@ -787,6 +787,32 @@ def test_lds_tiles_bit_identical(dev, k_split):
         assert torch.equal(ys[t], ys[2]), t
 
 
+# W8A16 (e4m3 weights, bf16 activations): the LDS tiles DMA the weight bytes and widen them at the
+# fragment reads with the k assignment of the 256x256 ping-pong W8A16 tile, so all of them agree
+# with it bit for bit (K a multiple of 128; K split planes of 128).
+@pytest.mark.parametrize("k_split", [1, 2])
+def test_w8a16_lds_tiles_bit_identical(dev, k_split):
+    counts = [33, 0, 64, 65, 97, 300, 1, 7 * 64 + 5]
+    g = torch.Generator().manual_seed(321 + k_split)
+    H, I = 512, 256
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    T = 200
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    a_rows = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32).to(dev)
+    qgu, sgu = oracle.quantize_weights_fp8(torch.randn(E, 2 * I, H, generator=g) * 0.02)
+    qd, sd = oracle.quantize_weights_fp8(torch.randn(E, H, I, generator=g) * 0.02)
+    qgu, sgu, qd, sd, off_t = qgu.to(dev), sgu.to(dev), qd.to(dev), sd.to(dev), off_t.to(dev)
+    hs = {t: cpu(ops.gemm_gate_up_silu(x, qgu, off_t, rows, a_rows=a_rows, w_scale=sgu, tile=t)) for t in (1, 2, 3, 4, 6)}
+    for t in (2, 3, 4, 6):
+        assert torch.equal(hs[t], hs[1]), t
+    h = hs[1].to(dev)
+    ys = {t: cpu(ops.gemm_down(h, qd, off_t, rows, w_scale=sd, k_split=k_split, tile=t)) for t in (1, 2, 3, 4, 6)}
+    for t in (2, 3, 4, 6):
+        assert torch.equal(ys[t], ys[1]), t
+
+
 @pytest.mark.parametrize("tile", [1, 2, 6])
 def test_fp8_gemms_remainder_tile_heights(dev, tile):
     """The same segment layouts on the W8A8 (fp8 x fp8) and W8A16 (fp8 weights) kernels."""
