@@ -1352,9 +1352,13 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8w_kernel(GemmA
 // and widened to bf16 at the fragment reads, the k assignment of the ping-pong W8A16 tile (within a
 // 64-k activation slab lane group q takes k = 16q + 8*KK + 0..7 in MFMA step KK; one 16-byte weight
 // read per slab covers both steps), so its sums are those of the 256x256 W8A16 tile, bit for bit.
-// A weight chunk serves two activation slabs: its DMA goes out at the top of the odd slab before
-// them, into the stage the chunk before last has left.  Both stages of each operand are distinct
-// objects and the loop is unrolled by four, so every stage index is static.  K % 128 == 0.
+// Tiles of at most 64 rows keep a whole 128-k chunk of both operands per stage (two activation
+// slabs and one weight slab, one barrier per chunk: Mixtral-8x7B 64 tokens, 32x128, gate/up 180.9
+// -> 162.7 us and down 98.3 -> 75.1 us against a barrier per activation slab).  The 128x128 tile,
+// whose chunk stages would leave one workgroup per CU, keeps 64-k activation stages: a weight chunk
+// serves two of them and its DMA goes out at the top of the odd slab before them, into the stage
+// the chunk before last has left.  Both stages of each operand are distinct objects and the loops
+// are unrolled, so every stage index is static.  K % 128 == 0.
 template <class G, int MBE>
 __device__ __forceinline__ void w8a16_slab_mma(f32x4_t (&acc)[MBE][G::NB], const uint16_t* sA, const uint16_t* sB,
                                                int half, int wm, int wn, int lane) {
@@ -1409,8 +1413,11 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_w8a16_dma_kernel(
   constexpr int B_PW = BN / 8 / NW;
   static_assert(A_PW * 8 * NW == BM && B_PW * 8 * NW == BN, "slab split over waves");
 
-  __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * BK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * BK];
+  // CHUNK (tiles of at most 64 rows): a stage holds a whole 128-k chunk of both operands (two
+  // activation slabs), one barrier per chunk; else a stage holds one 64-k activation slab.
+  constexpr bool CHUNK = BM <= 64;
+  __shared__ __attribute__((aligned(1024))) uint16_t sA0[(CHUNK ? 2 : 1) * BM * BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sA1[(CHUNK ? 2 : 1) * BM * BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * BK];   // BN rows of 128 e4m3 bytes
   __shared__ __attribute__((aligned(1024))) uint16_t sB1[BN * BK];
   __shared__ int s_pref[kMaxSeg + 1];
@@ -1448,6 +1455,36 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_w8a16_dma_kernel(
     for (int i = 0; i < MBE; ++i)
 #pragma unroll
       for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (CHUNK) {
+      auto issue_chunk = [&](int c, uint16_t* sa, uint16_t* sb) __attribute__((always_inline)) {
+        issue_a_dma<A_CNT, NW>(rA, a_voff, sa, wave, c * 256);
+        issue_a_dma<A_CNT, NW>(rA, a_voff, sa + BM * BK, wave, c * 256 + 128);
+        issue_b8_dma<B_PW, NW>(rB, b_voff, sb, wave, c * 128, nt);
+      };
+      auto chunk_mma = [&](const uint16_t* sa, const uint16_t* sb) __attribute__((always_inline)) {
+        w8a16_slab_mma<G, MBE>(acc, sa, sb, 0, wm, wn, lane);
+        w8a16_slab_mma<G, MBE>(acc, sa + BM * BK, sb, 1, wm, wn, lane);
+      };
+      // chunk c in stage 0 at the top of each iteration; the second load is unconditional (near
+      // the end it re-reads the last chunk into stage 0, which is not read again and which the
+      // closing barrier waits for)
+      issue_chunk(0, sA0, sB0);
+      __syncthreads();
+      int c = 0;
+      for (; c + 1 < NC; c += 2) {
+        issue_chunk(c + 1, sA1, sB1);
+        pin_issue();
+        chunk_mma(sA0, sB0);
+        __syncthreads();
+        issue_chunk(min(c + 2, NC - 1), sA0, sB0);
+        pin_issue();
+        chunk_mma(sA1, sB1);
+        __syncthreads();
+      }
+      if (c < NC) chunk_mma(sA0, sB0);
+      epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale, nullptr);   // bf16 activations
+      return;
+    }
     issue_a_dma<A_CNT, NW>(rA, a_voff, sA0, wave, 0);
     issue_b8_dma<B_PW, NW>(rB, b_voff, sB0, wave, 0, nt);
     __syncthreads();
@@ -1666,17 +1703,17 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
   if (ops == 2) {
     // W8A16: the LDS tiles DMA the e4m3 weights and widen them at the fragment reads, the
     // streaming kernel widens them in registers on the way to the MFMA.  Experts too large for
-    // the caches, measured on the routed Mixtral-8x7B segments (single GEMMs, cold, one box; us):
-    // gate/up streams below 12 expected rows per segment (32 tokens: 174.9 against 175.0 on
-    // 16x64), then 32x128 (64 tokens: 178.8 against 208.6 streamed), 64x128 from 24 rows (128
-    // tokens: 199.7 against 214.2 on 128x128), 128x128 from 48 (256 tokens: 250.4 against 265.0);
-    // the down projection (K split 2) streams below 12 rows (32 tokens: 88.1 against 93.3 on
-    // 16x64), then 128x128 (64 tokens: 97.9 against 106.7 streamed).  Smaller experts: streaming
-    // below 24 rows (the Qwen3-30B-A3B share at 32 and 256 tokens, gate/up 24 / 34 us against 37 /
-    // 38 on 32x128 with the weights widened through registers), 128x128 from 24.
+    // the caches, measured on the routed Mixtral-8x7B segments (cold, one box; us): streaming
+    // below one expected row per segment (1-3 tokens), then 32x128 (64 tokens, single GEMMs:
+    // gate/up 162.7 against 208.7 streamed, down with K split 2 75.1 against 106.5), 64x128 from
+    // 24 rows (128 tokens: 186.1 / 87.2 against 214.2 / 108.7 on 128x128), 128x128 from 48 (256
+    // tokens: 248.8 / 117.3 against 257.3 / 140.5 on 64x128); layers at 4 / 8 / 32 / 64 / 128 tokens
+    // 206 / 207 / 273 / 293 / 327 -> 185 / 190 / 233 / 260 / 302 us against streaming below 12 rows.
+    // Smaller experts: streaming below 24 rows (the Qwen3-30B-A3B share at 32 and 256 tokens,
+    // gate/up 24 / 34 us against 37 / 38 on 32x128 with the weights widened through registers),
+    // 128x128 from 24.
     if (expert_bytes >= 32.0 * 1024 * 1024)
-      tile = epi_silu(epi) ? (avg < 12 ? kTileXS : avg < 24 ? kTileS : avg < 48 ? kTileMS : avg < 128 ? kTileM : kTileL)
-                           : (avg < 12 ? kTileXS : avg < 128 ? kTileM : kTileL);
+      tile = avg < 1 ? kTileXS : avg < 24 ? kTileS : avg < 48 ? kTileMS : avg < 128 ? kTileM : kTileL;
     else
       tile = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
     if (tile == kTileL && (static_cast<long long>(p.max_rows) / 256 + p.S) * (p.N / gemm_out_cols_per_tile(kTileL, epi)) *
