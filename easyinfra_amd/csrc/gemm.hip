@@ -1700,6 +1700,7 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
                      (p.S > 0 ? p.S : 1);
   const double expert_bytes = static_cast<double>(p.nb_rows) * p.K * p.k_split * (b_fp8 ? 1 : 2);
   int tile;
+  bool keep_xs = false;   // a 16x64 choice that is not to be streamed
   if (ops == 2) {
     // W8A16: the LDS tiles DMA the e4m3 weights and widen them at the fragment reads, the
     // streaming kernel widens them in registers on the way to the MFMA.  Experts too large for
@@ -1709,13 +1710,20 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
     // 24 rows (128 tokens: 186.1 / 87.2 against 214.2 / 108.7 on 128x128), 128x128 from 48 (256
     // tokens: 248.8 / 117.3 against 257.3 / 140.5 on 64x128); layers at 4 / 8 / 32 / 64 / 128 tokens
     // 206 / 207 / 273 / 293 / 327 -> 185 / 190 / 233 / 260 / 302 us against streaming below 12 rows.
-    // Smaller experts: streaming below 24 rows (the Qwen3-30B-A3B share at 32 and 256 tokens,
-    // gate/up 24 / 34 us against 37 / 38 on 32x128 with the weights widened through registers),
-    // 128x128 from 24.
-    if (expert_bytes >= 32.0 * 1024 * 1024)
+    // Experts that stay in cache read half the bytes of their bf16 form, so the smaller tiles keep
+    // the CUs busy longer: 16x64 from one row (not streamed), 32x128 from 4, 64x128 from 20, the
+    // down projection on 128x128 from 100 and both on 256x256 from 256 (gate/up / down us,
+    // single GEMMs, cold: Qwen3-30B-A3B share 256 tokens 26.1 / 17.9 on 32x128 against 37.3 /
+    // 22.8 streamed, 768 tokens 29.7 / 27.3 on 64x128 against 39.8 / 36.2 on 128x128, 2048 tokens
+    // 48.9 on 64x128 / 39.0 on 128x128 against 53.8 / 52.6 on 256x256; DeepSeek-V2-Lite 768 tokens
+    // 108.8 / 66.9 on 64x128 against 125.9 / 78.9 on 128x128).
+    if (expert_bytes >= 32.0 * 1024 * 1024) {
       tile = avg < 1 ? kTileXS : avg < 24 ? kTileS : avg < 48 ? kTileMS : avg < 128 ? kTileM : kTileL;
-    else
-      tile = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    } else {
+      tile = avg < 4 ? kTileXS : avg < 20 ? kTileS : avg < 100 ? kTileMS : avg < 256 ? (epi_silu(epi) ? kTileMS : kTileM)
+                                                                                       : kTileL;
+      keep_xs = avg >= 1;
+    }
     if (tile == kTileL && (static_cast<long long>(p.max_rows) / 256 + p.S) * (p.N / gemm_out_cols_per_tile(kTileL, epi)) *
                                   p.k_split < kNumCu)
       tile = kTileM;
@@ -1730,7 +1738,7 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
   // 0.184-0.194 / 0.260 ms); 1 and 2 tokens stream (their layers 7 and 31 us slower on the LDS
   // tiles), 4 tokens measured either way by 10 % on two boxes.
   const bool w8a8_lds = ops == 1 && expert_bytes >= 32.0 * 1024 * 1024 && avg >= 2.0;
-  if (tile == kTileXS && stream_ok && !w8a8_lds) tile = kTileStream;
+  if (tile == kTileXS && stream_ok && !w8a8_lds && !keep_xs) tile = kTileStream;
   return tile;
 }
 
