@@ -1629,20 +1629,24 @@ int gemm_out_cols_per_tile(int tile, int epi) {
 //    174.3 / 178.6 / 218.9 on 64x128 / 128x128 / 32x128, down 88.2 against 99.5 / 105.1 / 115.3
 //    (uniform routing: 168.7 and 87.2 on 256x256); 128 tokens (12 rows): gate/up 112.6 on 128x128
 //    against 125.3 streamed and 128.4 on 32x128.
-static int routed_small_gate_up_tile(const GemmArgs& p, int S, double avg, int t) {
+static int routed_small_gate_up_tile(const GemmArgs& p, int S, double avg, int t, bool fp8) {
   const long long tiles_l = static_cast<long long>(S) * static_cast<long long>((avg + 255) / 256) * (p.N / 128);
   const long long tiles_m = static_cast<long long>(S) * static_cast<long long>((avg + 127) / 128) * (p.N / 64);
+  const long long tiles_ms = static_cast<long long>(S) * static_cast<long long>((avg + 63) / 64) * (p.N / 64);
   if (avg >= 40 && tiles_l >= kNumCu) return kTileL;
-  if (avg >= 20 && avg < 64) return kTileMS;
+  if (avg >= 20 && avg < 64 && (!fp8 || tiles_ms <= 3 * kNumCu)) return kTileMS;
   if (avg >= 8 && avg < 20 && tiles_m >= 2 * kNumCu) return kTileM;
   return t;
 }
 
-static int routed_small_down_tile(const GemmArgs& p, int S, double avg) {
+// e4m3 (W8A8) tiles do half the MFMA work per weight byte: the 64x128 band reaches to 80 rows, the
+// 256x256 tile takes over from 64, and below 40 rows the 32x128 tile (t) stays.
+static int routed_small_down_tile(const GemmArgs& p, int S, double avg, int t, bool fp8) {
   const long long tiles_ms = static_cast<long long>(S) * static_cast<long long>((avg + 63) / 64) * (p.N / 128);
   const long long tiles_l = static_cast<long long>(S) * static_cast<long long>((avg + 255) / 256) * (p.N / 256);
-  if (avg >= 20 && avg < 64 && tiles_ms <= 3 * kNumCu) return kTileMS;   // one round of 64x128 workgroups
-  if (avg >= 36 && tiles_l >= 2 * kNumCu) return kTileL;
+  if (avg >= 20 && avg < (fp8 ? 80 : 64) && tiles_ms <= 3 * kNumCu) return kTileMS;   // one round of 64x128 workgroups
+  if (avg >= (fp8 ? 64 : 36) && tiles_l >= 2 * kNumCu) return kTileL;
+  if (fp8 && avg < 40) return t;
   return kTileM;
 }
 
@@ -1678,10 +1682,10 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
     // tokens (~3900 local rows, 56-551 per expert) measured 72 us on 256x256 tiles and 89 us on
     // 128x128 (the expected 125 rows per expert would pick the latter).
     t = avg_bound >= 256 ? kTileL : avg_bound >= 96 ? kTileM : avg_bound >= 24 ? kTileS : kTileXS;
-    if (!b_fp8 && S >= 8 && avg_bound < 256) t = routed_small_gate_up_tile(p, S, avg, t);
+    if (S >= 8 && avg_bound < 256) t = routed_small_gate_up_tile(p, S, avg, t, b_fp8);
   } else {
     t = avg < 6 ? kTileXS : avg < 96 ? kTileS : avg < 384 ? kTileM : kTileL;
-    if (!b_fp8 && S >= 8 && avg >= 8 && avg < 384) t = routed_small_down_tile(p, S, avg);
+    if (S >= 8 && avg >= (b_fp8 ? 20 : 8) && avg < 384) t = routed_small_down_tile(p, S, avg, t, b_fp8);
   }
   if (t == kTileL) {
     // fewer 256x256 tiles than CUs (a dense shared-expert launch, say) leaves CUs idle: step down
