@@ -1734,6 +1734,11 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
     while (tile != kTileXS && p.N % gemm_out_cols_per_tile(tile, epi) != 0) tile = tile_step_down(tile);
   } else {
     tile = gemm_pick_tile(p, epi, b_fp8);
+    // The bf16 down projection of experts that stay in cache, from one expected row per segment:
+    // the 16x64 LDS tile rather than streaming (single launches, cold, one box: DeepSeek-V2-Lite 16
+    // / 32 tokens 32.9 / 39.0 us against 43.2 / 43.2 streamed, the Qwen3-30B-A3B share at 32 / 64
+    // tokens 25.2 / 28.9 against 25.9 / 31.1; at half a row streaming stays ahead, 19.8 against 21.8).
+    keep_xs = ops == 0 && !epi_silu(epi) && expert_bytes < 32.0 * 1024 * 1024 && avg >= 1;
   }
   // a few rows per segment: stream the weights instead of tiling them through LDS, except W8A8 on
   // experts too large for the caches, whose LDS tiles read the weights non-temporally: from two
