@@ -787,6 +787,32 @@ def test_lds_tiles_bit_identical(dev, k_split):
         assert torch.equal(ys[t], ys[2]), t
 
 
+# W8A16 with K not a multiple of 128 (one 64-k weight slab left over): the LDS tiles widen the
+# weights through registers instead (gate/up K = H = 192, down K = I = 192).
+@pytest.mark.parametrize("tile", [2, 3, 4, 6])
+def test_w8a16_lds_tiles_k_not_multiple_of_128(dev, tile):
+    counts = [20, 0, 70, 5]
+    g = torch.Generator().manual_seed(40 + tile)
+    E = len(counts)
+    off, off_t = _segments(counts)
+    rows = int(off[-1])
+    Hg, Ig = 192, 256   # gate/up: K = 192
+    Hd, Id = 256, 192   # down: K = 192
+    x = torch.randn(rows, Hg, generator=g).to(torch.bfloat16)
+    qgu, sgu = oracle.quantize_weights_fp8(torch.randn(E, 2 * Ig, Hg, generator=g) * 0.02)
+    qd, sd = oracle.quantize_weights_fp8(torch.randn(E, Hd, Id, generator=g) * 0.02)
+    hin = torch.randn(rows, Id, generator=g).to(torch.bfloat16)
+    h = cpu(ops.gemm_gate_up_silu(x.to(dev), qgu.to(dev), off_t.to(dev), rows, w_scale=sgu.to(dev), tile=tile)).float()
+    y = cpu(ops.gemm_down(hin.to(dev), qd.to(dev), off_t.to(dev), rows, w_scale=sd.to(dev), tile=tile))[0]
+    for e in range(E):
+        a, b = int(off[e]), int(off[e + 1])
+        if b == a:
+            continue
+        gu = (x[a:b].float() @ qgu[e].float().T) * sgu[e]
+        torch.testing.assert_close(h[a:b], oracle.silu(gu[:, :Ig]) * gu[:, Ig:], rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(y[a:b], (hin[a:b].float() @ qd[e].float().T) * sd[e], rtol=1e-3, atol=1e-3)
+
+
 # W8A16 (e4m3 weights, bf16 activations): the LDS tiles DMA the weight bytes and widen them at the
 # fragment reads with the k assignment of the 256x256 ping-pong W8A16 tile, so all of them agree
 # with it bit for bit (K a multiple of 128; K split planes of 128).
