@@ -1520,11 +1520,11 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
   long long grid = (total + kNumXcd - 1) / kNumXcd * kNumXcd;
   if (grid < kNumXcd) grid = kNumXcd;
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
-  // A plain runtime branch: both kernels of a configuration are instantiated together.
-  if (BFP8 && a_fp8)
+  // A plain runtime branch: the kernels of a configuration are instantiated together.
+  if (BFP8 && a_fp8) {
     hipLaunchKernelGGL((grouped_gemm_fp8_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
-  else if (BFP8) {
+  } else if (BFP8) {
     // W8A16: the e4m3 weights DMA'd to LDS and widened at the fragment reads when K allows, else
     // widened through registers on their way to LDS
     if constexpr (BM <= 128) {
@@ -1536,10 +1536,10 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
     }
     hipLaunchKernelGGL((grouped_gemm_fp8w_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
-  }
-  else
+  } else {
     hipLaunchKernelGGL((grouped_gemm_dma_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
+  }
   return hipGetLastError();
 }
 
