@@ -1673,10 +1673,13 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
   int t;
   if (expert_bytes >= 32.0 * 1024 * 1024) {
     // (W8A8 gate/up at 16 rows per expert on the routed, gathered rows of a Mixtral-8x7B
-    // decode batch: 182 us on 32x128 tiles, 190 us streamed)
+    // decode batch: 182 us on 32x128 tiles, 190 us streamed.  bf16 down projection on 128x128
+    // with its K split 2 from 4 expected rows, streaming below: Mixtral-8x7B layers at 16 / 20 /
+    // 24 / 28 tokens 488 / 499 / 492 / 499 -> 459 / 456 / 462 / 458 us cold, where streaming with a
+    // K split of 8 had run to 8 rows; 12 and 32 tokens unchanged)
     if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 128 ? kTileM : kTileL;
     else if (silu) t = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
-    else t = avg < 8 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    else t = avg < 4 ? kTileXS : avg < 128 ? kTileM : kTileL;
   } else if (silu) {
     // From the row bound, not the expected rows: the Qwen3-30B-A3B 32-expert share at 2048
     // tokens (~3900 local rows, 56-551 per expert) measured 72 us on 256x256 tiles and 89 us on
