@@ -141,6 +141,34 @@ def test_fp8_mixtral_real_shape(dev, T):
     assert res["w8a8"][0] <= 7.5e-2 and res["w8a8"][2] <= 7.5e-2
 
 
+# The fp8 modes on cache-resident experts at a mid-size batch, at the real shapes (Qwen3-30B-A3B
+# 32-expert share and DeepSeek-V2-Lite's routed experts, 768 tokens): the W8A16 LDS tiles that DMA
+# the e4m3 weights and the tile rules for these launches, against the oracle's own fp8 forward.
+@pytest.mark.parametrize("name", ["qwen3-30b-a3b-local32", "deepseek-v2-lite"])
+def test_fp8_small_experts_real_shape(dev, name):
+    import json
+    T = 768
+    s = SHAPES[name]
+    inp = make_inputs(s, T, device=dev)
+    qgu, sgu = ops.quantize_weights_fp8(inp.w_gate_up)
+    qd, sd = ops.quantize_weights_fp8(inp.w_down)
+    x, lg = cpu(inp.x), cpu(inp.logits)
+    ref = oracle.moe_forward(x, lg, s.top_k, cpu(inp.w_gate_up), cpu(inp.w_down), s.renormalize,
+                             expert_range=inp.expert_range)
+    for mode in ("w8a16", "w8a8"):
+        out = cpu(ops.fused_moe(inp.x, inp.logits, s.top_k, qgu, qd, renormalize=s.renormalize,
+                                expert_range=inp.expert_range, w_scales=(sgu, sd), out_dtype=torch.float32,
+                                w8a8=(mode == "w8a8")))
+        own = oracle.moe_forward_fp8(x, lg, s.top_k, cpu(qgu), cpu(sgu), cpu(qd), cpu(sd), s.renormalize, mode=mode,
+                                     expert_range=inp.expert_range)
+        r_own, r_ref = oracle.rel_l2(out, own), oracle.rel_l2(out, ref)
+        print("PARITY " + json.dumps({"case": f"{name} {mode} T={T} (routed experts)", "rows": T,
+                                      "rel_l2_vs_bf16_ref": r_ref, "rel_l2_vs_fp8_oracle": r_own}, sort_keys=True),
+              flush=True)
+        assert r_own <= 1e-2
+        assert r_ref <= (5e-2 if mode == "w8a16" else 7.5e-2)
+
+
 # The W8A8 layer's activation quantisation does not depend on how the routing was obtained or on
 # x's alignment (16-byte aligned rows take the register quantiser, others the two-pass one): the
 # layer routed here, routed by the caller (EIMOE_ROUTING_IN) and run on x 8 bytes past a 16-byte
