@@ -1676,9 +1676,11 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
     // decode batch: 182 us on 32x128 tiles, 190 us streamed.  bf16 down projection on 128x128
     // with its K split 2 from 4 expected rows, streaming below: Mixtral-8x7B layers at 16 / 20 /
     // 24 / 28 tokens 488 / 499 / 492 / 499 -> 459 / 456 / 462 / 458 us cold, where streaming with a
-    // K split of 8 had run to 8 rows; 12 and 32 tokens unchanged)
+    // K split of 8 had run to 8 rows; 12 and 32 tokens unchanged.  bf16 gate/up on 256x256 from 64
+    // rows: layers at 256 / 320 / 384 / 448 tokens 524 / 543 / 555 / 578 -> 511 / 516 / 544 / 552 us
+    // cold against 128x128 up to 128 rows; 192 tokens unchanged)
     if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 128 ? kTileM : kTileL;
-    else if (silu) t = avg < 24 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    else if (silu) t = avg < 24 ? kTileXS : avg < 64 ? kTileM : kTileL;
     else t = avg < 4 ? kTileXS : avg < 128 ? kTileM : kTileL;
   } else if (silu) {
     // From the row bound, not the expected rows: the Qwen3-30B-A3B 32-expert share at 2048
