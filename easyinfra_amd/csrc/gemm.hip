@@ -1678,8 +1678,9 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
     // 24 / 28 tokens 488 / 499 / 492 / 499 -> 459 / 456 / 462 / 458 us cold, where streaming with a
     // K split of 8 had run to 8 rows; 12 and 32 tokens unchanged.  bf16 gate/up on 256x256 from 64
     // rows: layers at 256 / 320 / 384 / 448 tokens 524 / 543 / 555 / 578 -> 511 / 516 / 544 / 552 us
-    // cold against 128x128 up to 128 rows; 192 tokens unchanged)
-    if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 128 ? kTileM : kTileL;
+    // cold against 128x128 up to 128 rows; 192 tokens unchanged.  W8A8 likewise on 256x256 from 64
+    // rows: 256 / 320 / 384 / 448 tokens 323 / 340 / 355 / 368 -> 316 / 316 / 334 / 342 us)
+    if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 64 ? kTileM : kTileL;
     else if (silu) t = avg < 24 ? kTileXS : avg < 64 ? kTileM : kTileL;
     else t = avg < 4 ? kTileXS : avg < 128 ? kTileM : kTileL;
   } else if (silu) {
@@ -1716,9 +1717,10 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
     // the caches, measured on the routed Mixtral-8x7B segments (cold, one box; us): streaming
     // below one expected row per segment (1-3 tokens), then 32x128 (64 tokens, single GEMMs:
     // gate/up 162.7 against 208.7 streamed, down with K split 2 75.1 against 106.5), 64x128 from
-    // 24 rows (128 tokens: 186.1 / 87.2 against 214.2 / 108.7 on 128x128), 128x128 from 48 (256
-    // tokens: 248.8 / 117.3 against 257.3 / 140.5 on 64x128); layers at 4 / 8 / 32 / 64 / 128 tokens
-    // 206 / 207 / 273 / 293 / 327 -> 185 / 190 / 233 / 260 / 302 us against streaming below 12 rows.
+    // 24 rows (128 tokens: 186.1 / 87.2 against 214.2 / 108.7 on 128x128; 192 tokens: layer 334 ->
+    // 304 us against 128x128 from 48 rows), 128x128 from 56 (256 tokens: 248.8 / 117.3 against
+    // 257.3 / 140.5 on 64x128); layers at 4 / 8 / 32 / 64 / 128 tokens 206 / 207 / 273 / 293 / 327 ->
+    // 185 / 190 / 233 / 260 / 302 us against streaming below 12 rows.
     // Experts that stay in cache read half the bytes of their bf16 form, so the smaller tiles keep
     // the CUs busy longer: 16x64 from one row (not streamed), 32x128 from 4, 64x128 from 20, the
     // down projection on 128x128 from 100 and both on 256x256 from 256 (gate/up / down us,
@@ -1727,7 +1729,7 @@ int gemm_choose_tile(const GemmArgs& p, int epi, bool b_fp8, bool a_fp8) {
     // 48.9 on 64x128 / 39.0 on 128x128 against 53.8 / 52.6 on 256x256; DeepSeek-V2-Lite 768 tokens
     // 108.8 / 66.9 on 64x128 against 125.9 / 78.9 on 128x128).
     if (expert_bytes >= 32.0 * 1024 * 1024) {
-      tile = avg < 1 ? kTileXS : avg < 24 ? kTileS : avg < 48 ? kTileMS : avg < 128 ? kTileM : kTileL;
+      tile = avg < 1 ? kTileXS : avg < 24 ? kTileS : avg < 56 ? kTileMS : avg < 128 ? kTileM : kTileL;
     } else {
       tile = avg < 4 ? kTileXS : avg < 20 ? kTileS : avg < 100 ? kTileMS : avg < 256 ? (epi_silu(epi) ? kTileMS : kTileM)
                                                                                        : kTileL;
