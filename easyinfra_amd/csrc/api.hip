@@ -140,15 +140,34 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
   // tile, which takes a quarter, half or full height (a short tile costs its share of a round)
   const int segs = std::max(1, std::min(n_local, rows));
   const double per = static_cast<double>(rows) / segs;
-  const double rem = per - std::floor(per / bm) * bm;
-  const double rem_tile = rem <= 0.0 ? 0.0 : rem <= bm / 4 ? 0.25 : rem <= bm / 2 ? 0.5 : 1.0;
-  const double mt = segs * (std::floor(per / bm) + rem_tile);
+  double mt;
+  if (tile == kTileL) {
+    // The persistent 256x256 kernel: every m-tile of a segment costs about a full tile whatever its
+    // height, and routed segments scatter around the mean, so an expected count just past a
+    // multiple of 256 rows gives about half the segments one more m-tile.  Count
+    // E[ceil(rows / 256)] with the rows ~ normal(mean, sqrt(mean)).
+    const double sd = std::sqrt(std::max(per, 1.0));
+    double e = 0.0;
+    for (int j = 0; j * static_cast<double>(bm) < per + 6.0 * sd; ++j)
+      e += 0.5 * std::erfc((j * static_cast<double>(bm) + 0.5 - per) / (sd * std::sqrt(2.0)));
+    mt = segs * e;
+  } else {
+    // m-tiles in full-tile units from the expected rows per segment: whole tiles plus the
+    // remainder's tile, which takes a quarter, half or full height (a short tile costs its share)
+    const double rem = per - std::floor(per / bm) * bm;
+    const double rem_tile = rem <= 0.0 ? 0.0 : rem <= bm / 4 ? 0.25 : rem <= bm / 2 ? 0.5 : 1.0;
+    mt = segs * (std::floor(per / bm) + rem_tile);
+  }
   const double work = mt * (H / bn);                                              // full-tile units
   const long long tiles = static_cast<long long>(segs * std::ceil(per / bm)) * (H / bn);   // workgroups
   constexpr double kTileFlops = 4.7e12;   // measured bf16 GEMM rate per CU, FLOP/s
   constexpr double kHbm = 5.0e12;         // achieved HBM rate for plane traffic, B/s
   const double t_tile = 2.0 * bm * bn * static_cast<double>(I) / kTileFlops;
   const double t_plane = 2.0 * static_cast<double>(max_rows) * H * y_elem / kHbm;
+  // Four or more rounds of full-K 256x256 tiles: the partial last round costs little under the
+  // power-limited clock, and each extra plane is a round trip of the whole output (the Mixtral-8x7B
+  // 8192-token layer: one split)
+  if (tile == kTileL && work >= 4.0 * kNumCu) return 1;
   int best = 1;
   double best_cost = 1e300;
   for (int split = 1; split <= 8; split *= 2) {
@@ -156,7 +175,10 @@ int pick_down_split(int max_rows, int rows_hint, int n_local, int H, int I, int 
     const long long items = tiles * split;
     const double rounds = std::ceil(work * split / kNumCu);
     double cost = rounds / split * t_tile + (split - 1) * t_plane;
-    if (items < 2 * kNumCu && split < 8 && I % (128 * split) == 0) cost = 1e300;   // too few to fill the GPU
+    // too few workgroups to fill the GPU: twice over for the one-tile-per-workgroup kernels, once
+    // for the persistent 256x256 one (whose workgroups walk their tiles)
+    const bool few = tile == kTileL ? work * split < kNumCu : items < 2 * kNumCu;
+    if (few && split < 8 && I % (128 * split) == 0) cost = 1e300;
     if (cost < best_cost * 0.98) {
       best_cost = cost;
       best = split;
