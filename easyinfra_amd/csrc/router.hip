@@ -23,21 +23,22 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 }
 
 // The router fused with the many-workgroup align's first pass: workgroup b routes tokens
-// [b*TB, (b+1)*TB) (TB = 4 waves x 64/LPT tokens, one routing step per wave), which are the
+// [b*TB, (b+1)*TB) (TB = WPB waves x 64/LPT tokens, one routing step per wave), which are the
 // flat ids [b*TB*k, (b+1)*TB*k): align chunk b, whose per-expert counts it writes to
 // hist_g[b][n_loc] (LDS integer atomics: the counts do not depend on their order).
-template <int LPT, int VPL, int KMAX>
-__global__ __launch_bounds__(256) void router_hist_kernel(const float* __restrict__ logits, int T, int E, int k,
-                                                          int renorm, int32_t* __restrict__ ids,
-                                                          float* __restrict__ wts, int e_lo, int n_loc,
-                                                          int32_t* __restrict__ hist_g) {
+template <int LPT, int VPL, int KMAX, int WPB>
+__global__ __launch_bounds__(64 * WPB) void router_hist_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                               int renorm, int32_t* __restrict__ ids,
+                                                               float* __restrict__ wts, int e_lo, int n_loc,
+                                                               int32_t* __restrict__ hist_g) {
   extern __shared__ int s_hist[];   // [n_loc]
-  for (int i = threadIdx.x; i < n_loc; i += 256) s_hist[i] = 0;
+  for (int i = threadIdx.x; i < n_loc; i += 64 * WPB) s_hist[i] = 0;
   __syncthreads();
-  route_rows<LPT, VPL, KMAX, kLdsHist>(logits, T, E, k, renorm, ids, wts, s_hist, blockIdx.x * 4 + (threadIdx.x >> 6),
-                                       gridDim.x * 4, e_lo, n_loc);
+  route_rows<LPT, VPL, KMAX, kLdsHist>(logits, T, E, k, renorm, ids, wts, s_hist,
+                                       blockIdx.x * WPB + (threadIdx.x >> 6), gridDim.x * WPB, e_lo, n_loc);
   __syncthreads();
-  for (int e = threadIdx.x; e < n_loc; e += 256) hist_g[static_cast<long long>(blockIdx.x) * n_loc + e] = s_hist[e];
+  for (int e = threadIdx.x; e < n_loc; e += 64 * WPB)
+    hist_g[static_cast<long long>(blockIdx.x) * n_loc + e] = s_hist[e];
 }
 
 template <int LPT, int VPL>
@@ -57,14 +58,22 @@ static hipError_t launch_router_lv(const float* logits, int T, int E, int k, int
 
 template <int LPT, int VPL>
 static hipError_t launch_router_hist_lv(const float* logits, int T, int E, int k, int renorm, int32_t* ids, float* w,
-                                        int e_lo, int n_loc, int blocks, int32_t* hist, hipStream_t s) {
+                                        int e_lo, int n_loc, int blocks, int wpb, int32_t* hist, hipStream_t s) {
   const size_t lds = static_cast<size_t>(n_loc) * sizeof(int);
-  if (k <= 8)
-    hipLaunchKernelGGL((router_hist_kernel<LPT, VPL, 8>), dim3(blocks), dim3(256), lds, s, logits, T, E, k, renorm,
+  if (wpb == 8) {
+    if (k <= 8)
+      hipLaunchKernelGGL((router_hist_kernel<LPT, VPL, 8, 8>), dim3(blocks), dim3(512), lds, s, logits, T, E, k,
+                         renorm, ids, w, e_lo, n_loc, hist);
+    else
+      hipLaunchKernelGGL((router_hist_kernel<LPT, VPL, 32, 8>), dim3(blocks), dim3(512), lds, s, logits, T, E, k,
+                         renorm, ids, w, e_lo, n_loc, hist);
+  } else if (k <= 8) {
+    hipLaunchKernelGGL((router_hist_kernel<LPT, VPL, 8, 4>), dim3(blocks), dim3(256), lds, s, logits, T, E, k, renorm,
                        ids, w, e_lo, n_loc, hist);
-  else
-    hipLaunchKernelGGL((router_hist_kernel<LPT, VPL, 32>), dim3(blocks), dim3(256), lds, s, logits, T, E, k, renorm,
+  } else {
+    hipLaunchKernelGGL((router_hist_kernel<LPT, VPL, 32, 4>), dim3(blocks), dim3(256), lds, s, logits, T, E, k, renorm,
                        ids, w, e_lo, n_loc, hist);
+  }
   return hipGetLastError();
 }
 
@@ -74,6 +83,7 @@ static int topk_lanes(int E) { return E <= 8 ? 8 : E <= 128 ? 16 : E <= 256 ? 32
 struct RouteHistPlan {
   int blocks;   // 0: not used
   int chunk;    // flat ids per workgroup
+  int wpb;      // waves per workgroup (4 or 8)
 };
 
 // Each placing workgroup sums the whole chunk-count matrix, so the matrix is kept small:
@@ -82,19 +92,28 @@ struct RouteHistPlan {
 // us, at 2048 tokens (4096 cells) equal, DeepSeek-V2-Lite 4096 tokens (16384 cells) 611 -> 620 us.
 constexpr long long kRouteHistMaxCells = 2048;
 
+// Workgroups of 4 waves, or of 8 where that keeps the matrix within bounds (the Qwen3-30B-A3B
+// share at 1536 / 2048 tokens: 1536 / 2048 cells of 8-wave workgroups instead of the router, the
+// histogram launch and the place launch; layers 125.7 / 133.0 -> 122.8 / 130.3 us cold, one box).
 static RouteHistPlan route_hist_plan(int T, int E, int k, int n_loc) {
-  RouteHistPlan r{0, 0};
-  const int tb = 4 * (64 / topk_lanes(E));   // tokens per workgroup: one routing step per wave
-  const long long blocks = (static_cast<long long>(T) + tb - 1) / tb;
-  if (blocks < 2 || blocks * n_loc > kRouteHistMaxCells) return r;
-  r.blocks = static_cast<int>(blocks);
-  r.chunk = tb * k;
+  RouteHistPlan r{0, 0, 0};
+  for (int wpb = 4; wpb <= 8; wpb *= 2) {
+    const int tb = wpb * (64 / topk_lanes(E));   // tokens per workgroup: one routing step per wave
+    const long long blocks = (static_cast<long long>(T) + tb - 1) / tb;
+    if (blocks < 2) return r;
+    if (blocks * n_loc > kRouteHistMaxCells) continue;
+    r.blocks = static_cast<int>(blocks);
+    r.chunk = tb * k;
+    r.wpb = wpb;
+    return r;
+  }
   return r;
 }
 
 static hipError_t launch_router_hist(const float* logits, int T, int E, int k, int renorm, int32_t* ids, float* w,
-                                     int e_lo, int n_loc, int blocks, int32_t* hist, hipStream_t s) {
-#define EIMOE_RH(L, V) return launch_router_hist_lv<L, V>(logits, T, E, k, renorm, ids, w, e_lo, n_loc, blocks, hist, s)
+                                     int e_lo, int n_loc, int blocks, int wpb, int32_t* hist, hipStream_t s) {
+#define EIMOE_RH(L, V) \
+  return launch_router_hist_lv<L, V>(logits, T, E, k, renorm, ids, w, e_lo, n_loc, blocks, wpb, hist, s)
   if (E <= 8) EIMOE_RH(8, 1);
   if (E <= 16) EIMOE_RH(16, 1);
   if (E <= 32) EIMOE_RH(16, 2);
@@ -390,7 +409,7 @@ hipError_t launch_route_align(const float* logits, int T, int E, int k, int reno
   if (!route_align_fused(T, E, k, n_loc)) {
     const RouteHistPlan rp = route_hist_plan(T, E, k, n_loc);
     if (hist != nullptr && rp.blocks > 0) {
-      hipError_t e = launch_router_hist(logits, T, E, k, renorm, ids, w, e_lo, n_loc, rp.blocks, hist, s);
+      hipError_t e = launch_router_hist(logits, T, E, k, renorm, ids, w, e_lo, n_loc, rp.blocks, rp.wpb, hist, s);
       if (e != hipSuccess) return e;
       return launch_align_place(ids, T, k, e_lo, n_loc, rp.blocks, rp.chunk, hist, counts, offsets, sorted_flat,
                                 sorted_tok, pos, s);

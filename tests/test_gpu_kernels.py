@@ -231,6 +231,10 @@ def test_align_out_of_window_ids_dropped(dev):
     # at most 64 routed pairs: the one-wave sort
     (1, 128, 8, 0, 32, True), (8, 128, 8, 32, 32, True), (3, 256, 8, 0, 256, False), (5, 64, 6, 16, 16, True),
     (32, 8, 2, 0, 8, True), (1, 8, 2, 6, 2, False), (4, 256, 16, 0, 256, True),
+    # larger batches: the router, then the one-workgroup align (this entry takes no workspace; the
+    # layer's many-workgroup paths are checked through its routing ids and outputs)
+    (600, 128, 8, 0, 32, True), (8192, 8, 2, 0, 8, True), (1536, 128, 8, 32, 32, True),
+    (2048, 128, 8, 0, 32, True), (2040, 128, 8, 96, 32, False),
 ])
 def test_route_align_bit_exact(dev, T, E, k, e_lo, n_loc, renorm):
     g = torch.Generator().manual_seed(T * 31 + E)
