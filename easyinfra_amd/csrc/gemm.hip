@@ -1143,9 +1143,11 @@ __global__ void __launch_bounds__(512) grouped_gemm_pp3p_kernel(GemmArgs p) {
   // A short tile (a quarter or half of the rows) of a segment that is a single m-tile is the only
   // reader of its weight panels: its weight DMA takes the non-temporal hint, as the LDS-tiled
   // kernels' decode launches do (bf16 and W8A8; the W8A16 loop stages its weights elsewhere).
-  // Cold layers, A/B on one box: Qwen3-30B-A3B share at 2048 tokens (28 of its 32 experts one short
-  // tile each) 9-10 % faster, DeepSeek-V2-Lite at 768 tokens 6-7 %, other workloads within 1 %;
-  // full-height single tiles with the hint as well measured the same.
+  // A/B on one box, with the LDS-tiled kernels' per-tile hint: layers timed back to back, Qwen3-30B-A3B
+  // share at 2048 tokens (28 of its 32 experts one short tile each) 0.138 -> 0.126 ms and
+  // DeepSeek-V2-Lite at 768 / 4096 tokens 0.327 -> 0.295 / 0.669 -> 0.649 ms; after a 512 MB write
+  // (dirty lines in the last-level cache) 9-16 % and 4-5 % faster; after a 512 MB read within 1 %.
+  // Full-height single tiles with the hint as well measured the same.
   auto nt_tile = [&](const TileCoord& t) {
     return MODE != 2 && t.one_mt != 0 && mbe_of_rows<256, MB, A_PW>(t.row_end - t.row0) < MB;
   };
