@@ -35,6 +35,7 @@
 //   * SiLU epilogue: a tile holds gate rows [n0, n0+BN/2) and the matching up rows
 //     [I+n0, ...); h = silu(g)*u is formed in registers and stored as bf16.
 #include <algorithm>
+#include <cmath>
 
 #include "common.h"
 #include "kernels.h"
@@ -744,6 +745,172 @@ __device__ __forceinline__ void pp_barrier() {
 }
 __device__ __forceinline__ void pp_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }     // vmcnt(0)
 __device__ __forceinline__ void pp_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }   // lgkmcnt(0)
+
+// ---------------------------------------------------------------------------- bf16: deeper LDS ring
+// s_waitcnt vmcnt(N), the other counters untouched (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Fragment reads of the ring kernel as inline ds_read_b128: the compiler's own waits for LDS DMA
+// cannot tell the ring's stages apart (with a DMA in flight into another stage it waited for all of
+// it before each read, whatever the barrier or the object layout), so the reads are hidden from it.
+// One asm statement issues all of a slab's N reads and waits for them (lgkmcnt(0)), so nothing the
+// compiler places between the reads and their use can see a register before its data has landed.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  typedef const __attribute__((address_space(3))) void* lds_cptr_t;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr_t)p));
+}
+template <int N>
+__device__ __forceinline__ void lds_read_wait(const uint32_t (&a)[N], bf16x8_t (&f)[N]) {
+  static_assert(N == 6 || N == 8 || N == 10 || N == 12, "fragment count of a ring slab");
+  if constexpr (N == 6) {
+    asm volatile("ds_read_b128 %0, %6\n ds_read_b128 %1, %7\n ds_read_b128 %2, %8\n ds_read_b128 %3, %9\n"
+                 " ds_read_b128 %4, %10\n ds_read_b128 %5, %11\n s_waitcnt lgkmcnt(0)"
+                 : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]));
+  } else if constexpr (N == 8) {
+    asm volatile("ds_read_b128 %0, %8\n ds_read_b128 %1, %9\n ds_read_b128 %2, %10\n ds_read_b128 %3, %11\n"
+                 " ds_read_b128 %4, %12\n ds_read_b128 %5, %13\n ds_read_b128 %6, %14\n ds_read_b128 %7, %15\n"
+                 " s_waitcnt lgkmcnt(0)"
+                 : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]),
+                   "=&v"(f[7])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
+  } else if constexpr (N == 10) {
+    asm volatile("ds_read_b128 %0, %10\n ds_read_b128 %1, %11\n ds_read_b128 %2, %12\n ds_read_b128 %3, %13\n"
+                 " ds_read_b128 %4, %14\n ds_read_b128 %5, %15\n ds_read_b128 %6, %16\n ds_read_b128 %7, %17\n"
+                 " ds_read_b128 %8, %18\n ds_read_b128 %9, %19\n s_waitcnt lgkmcnt(0)"
+                 : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]),
+                   "=&v"(f[7]), "=&v"(f[8]), "=&v"(f[9])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
+                   "v"(a[8]), "v"(a[9]));
+  } else {
+    asm volatile("ds_read_b128 %0, %12\n ds_read_b128 %1, %13\n ds_read_b128 %2, %14\n ds_read_b128 %3, %15\n"
+                 " ds_read_b128 %4, %16\n ds_read_b128 %5, %17\n ds_read_b128 %6, %18\n ds_read_b128 %7, %19\n"
+                 " ds_read_b128 %8, %20\n ds_read_b128 %9, %21\n ds_read_b128 %10, %22\n ds_read_b128 %11, %23\n"
+                 " s_waitcnt lgkmcnt(0)"
+                 : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]),
+                   "=&v"(f[7]), "=&v"(f[8]), "=&v"(f[9]), "=&v"(f[10]), "=&v"(f[11])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
+                   "v"(a[8]), "v"(a[9]), "v"(a[10]), "v"(a[11]));
+  }
+}
+
+// LDS byte addresses of a slab's fragments (both K halves: A then B of half 0, then of half 1), as
+// read_frags addresses them.
+template <class G, int MBE>
+__device__ __forceinline__ void ring_frag_addrs(uint32_t aA, uint32_t aB, int wm, int wn, int lane,
+                                                uint32_t (&ad)[2 * (MBE + G::NB)]) {
+  const int lr = lane & 15;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int c = kk * 4 + (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < MBE; ++i) {
+      const int R = wm * 16 * MBE + i * 16 + lr;
+      ad[kk * (MBE + G::NB) + i] = aA + 2 * (R * G::BK + ((c ^ swz(R)) << 3));
+    }
+#pragma unroll
+    for (int j = 0; j < G::NB; ++j) {
+      const int R = wn * G::WN + j * 16 + lr;
+      ad[kk * (MBE + G::NB) + MBE + j] = aB + 2 * (R * G::BK + ((c ^ swz(R)) << 3));
+    }
+  }
+}
+
+// grouped_gemm_dma_kernel on a ring of NS LDS stages: NS - 1 slabs in flight per workgroup instead
+// of one.  The two-stage loop's __syncthreads() fences wait for every DMA in flight at each slab
+// end; here each slab ends waiting for its wave's next slab only (loads complete in issue order)
+// and a barrier without a fence publishes it.  Same tiles, LDS layout per stage and accumulation
+// order: bit-identical results.  For launches whose tiles fit the GPU at the ring's occupancy.
+template <int BM, int BN, int WGM, int WGN, int EPI, int GM, int NS>
+__global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_ring_kernel(GemmArgs p) {
+  static_assert(NS == 3, "three stages");
+  using G = Geo<BM, BN, WGM, WGN, EPI>;
+  constexpr int EB = 2;
+  constexpr int BK = G::BK;
+  constexpr int NW = G::NW;
+  constexpr int A_PW = BM / 8 / G::NW;
+  constexpr int B_PW = BN / 8 / G::NW;
+  static_assert(A_PW * 8 * G::NW == BM && B_PW * 8 * G::NW == BN, "slab split over waves");
+  // One object per stage (A then B), read with static indices, so alias analysis proves that the
+  // DMA into one stage does not touch the one being read (with a separate object per operand and
+  // stage, nine in all, the compiler waited for the DMA just issued before every fragment read).
+  struct Stage {
+    uint16_t a[BM * BK];
+    uint16_t b[BN * BK];
+  };
+  __shared__ __attribute__((aligned(1024))) Stage t0;
+  __shared__ __attribute__((aligned(1024))) Stage t1;
+  __shared__ __attribute__((aligned(1024))) Stage t2;
+  __shared__ int s_pref[kMaxSeg + 1];
+
+  TileCoord tc;
+  if (!decode_tile<BM, G::OUT_BN, GM>(p, s_pref, tc)) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane >> 3;
+  const long long k0 = static_cast<long long>(tc.split) * p.K;
+  const BufRef rA{static_cast<const uint8_t*>(p.a) + k0 * EB, (p.a_rows_cap * p.lda - k0) * EB};
+  uint32_t a_voff[A_PW];
+  a_offsets<A_PW, NW>(p, tc, wave, lane, EB, a_voff);
+  const uint8_t* b_base = expert_weights(p, tc.expert, EB) + k0 * EB;
+  const BufRef rB{b_base, (p.b_estride - k0) * EB};
+  uint32_t b_voff[B_PW];
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i) {
+    const int R = (wave * B_PW + i) * 8 + lrow;
+    const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
+    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb * EB + (((lane & 7) ^ swz(R)) << 4));
+  }
+  const int wm = wave % WGM;
+  const int wn = wave / WGM;
+  const int KT = p.K * EB / (BK * 2);
+  const bool b_nt = p.b_nt != 0 || tc.one_mt != 0;
+  by_height<BM, G::MB, A_PW>(tc.row_end - tc.row0, [&]<int MBE>() {
+    constexpr int A_CNT = A_PW * MBE / G::MB;
+    constexpr int L = A_CNT + B_PW;   // DMA instructions per slab per wave
+    f32x4_t acc[MBE][G::NB];
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // slabs 0 and 1 into stages 0 and 1 (clamped to the last slab: stages not read again)
+    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, t0.a, t0.b, wave, 0, b_nt);
+    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, t1.a, t1.b, wave, min(1, KT - 1) * BK * 2, b_nt);
+    wait_vm<(NS - 2) * L>();   // this wave's slab 0
+    pp_barrier();
+    // slab kt + J: read stage J, load slab kt + J + NS - 1 into the stage slab kt + J - 1 read (every
+    // wave finished reading it before the barrier that ended that slab).
+    // The slab's DMA goes first, then its fragment reads and their wait (lds_read_wait), its MFMAs, and
+    // the wait for the next slab's data.
+#define EIMOE_RING_SLAB(J, SA, SB, SAN, SBN)                                                                \
+  if (kt + J < KT) {                                                                                        \
+    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, SAN, SBN, wave, min(kt + J + NS - 1, KT - 1) * BK * 2, \
+                                    b_nt);                                                                  \
+    uint32_t ad[2 * (MBE + G::NB)];                                                                         \
+    ring_frag_addrs<G, MBE>(lds_addr(SA), lds_addr(SB), wm, wn, lane, ad);                                  \
+    bf16x8_t fr[2 * (MBE + G::NB)];                                                                         \
+    lds_read_wait(ad, fr);                                                                                  \
+    mma<G, MBE>(acc, *reinterpret_cast<bf16x8_t(*)[MBE]>(fr), *reinterpret_cast<bf16x8_t(*)[G::NB]>(fr + MBE)); \
+    mma<G, MBE>(acc, *reinterpret_cast<bf16x8_t(*)[MBE]>(fr + MBE + G::NB),                                 \
+                *reinterpret_cast<bf16x8_t(*)[G::NB]>(fr + 2 * MBE + G::NB));                               \
+    wait_vm<(NS - 2) * L>();                                                                                \
+    pp_barrier();                                                                                           \
+  }
+    for (int kt = 0; kt < KT; kt += NS) {
+      EIMOE_RING_SLAB(0, t0.a, t0.b, t2.a, t2.b)
+      EIMOE_RING_SLAB(1, t1.a, t1.b, t0.a, t0.b)
+      EIMOE_RING_SLAB(2, t2.a, t2.b, t1.a, t1.b)
+    }
+#undef EIMOE_RING_SLAB
+    pp_wait_vm0();   // the clamped loads near the end land before the workgroup's LDS is released
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, nullptr, nullptr);
+  });
+}
 
 // ---------------------------------------------------------------------------- ping-pong, three B stages (bf16 or e4m3)
 // The ping-pong kernel with the weight panel (B, the operand streamed from HBM) fetched two slabs
@@ -1547,6 +1714,30 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_w8a16_dma_kernel(
 }
 
 // ---------------------------------------------------------------------------- launch
+// bf16 LDS tiles of at most 64 rows: the three-stage ring (grouped_gemm_ring_kernel) holds two slabs
+// in flight per workgroup instead of one, but at fewer workgroups per CU (LDS: 32x128 3 -> 2,
+// 64x128 3 -> 2, 16x64 6 -> 4).  Taken unless the two-stage kernel would run the launch's tiles in
+// one round and the ring would not: estimated tiles (expected rows, as the tile rules use them) above
+// the two-stage slots, or within the ring's with a third to spare for skewed routing.  A/B on one
+// box, all bit-identical, the ring on every such tile: DeepSeek-V2-Lite 64 / 256 tokens 0.184 ->
+// 0.170 / 0.222 -> 0.200 ms cold, Qwen3-30B-A3B share 256 tokens 95 -> 93 us, but the share at 768
+// tokens 90 -> 92 us (its down projection, ~640 tiles of 64x128, one round of the two-stage kernel's
+// 768 slots and 1.25 of the ring's 512).
+static int lds_tile_wgs(int bm, int bn, int stages) {
+  const int bytes = stages * (bm + bn) * 64 * 2 + (kMaxSeg + 1) * 4;
+  const int kib = (bytes + 1023) / 1024;
+  return 160 / kib;
+}
+
+static bool use_ring_tile(const GemmArgs& p, int bm, int bn, int n_tiles) {
+  const int S = p.S > 0 ? p.S : 1;
+  const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) / S;
+  const double est = static_cast<double>(S) * std::ceil(avg / bm) * n_tiles * p.k_split;
+  const double slots2 = static_cast<double>(lds_tile_wgs(bm, bn, 2)) * kNumCu;
+  const double slots3 = static_cast<double>(lds_tile_wgs(bm, bn, 3)) * kNumCu;
+  return est > slots2 || est * 1.3 <= slots3;
+}
+
 template <int BM, int BN, int WGM, int WGN, int EPI, bool BFP8, int GM>
 static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStream_t s) {
   constexpr int OUT_BN = epi_silu(EPI) ? BN / 2 : BN;
@@ -1573,6 +1764,13 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
     hipLaunchKernelGGL((grouped_gemm_fp8w_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
   } else {
+    if constexpr (BM <= 64) {
+      if (use_ring_tile(p, BM, BN, n_tiles)) {
+        hipLaunchKernelGGL((grouped_gemm_ring_kernel<BM, BN, WGM, WGN, EPI, GM, 3>), dim3(static_cast<unsigned>(grid)),
+                           dim3(WGM * WGN * 64), 0, s, p);
+        return hipGetLastError();
+      }
+    }
     hipLaunchKernelGGL((grouped_gemm_dma_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
   }
