@@ -765,7 +765,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 template <int N>
 __device__ __forceinline__ void lds_read_wait(const uint32_t (&a)[N], bf16x8_t (&f)[N]) {
-  static_assert(N == 6 || N == 8 || N == 10 || N == 12, "fragment count of a ring slab");
+  static_assert(N == 6 || N == 8 || N == 10 || N == 12 || N == 16, "fragment count of a ring slab");
   if constexpr (N == 6) {
     asm volatile("ds_read_b128 %0, %6\n ds_read_b128 %1, %7\n ds_read_b128 %2, %8\n ds_read_b128 %3, %9\n"
                  " ds_read_b128 %4, %10\n ds_read_b128 %5, %11\n s_waitcnt lgkmcnt(0)"
@@ -786,6 +786,17 @@ __device__ __forceinline__ void lds_read_wait(const uint32_t (&a)[N], bf16x8_t (
                    "=&v"(f[7]), "=&v"(f[8]), "=&v"(f[9])
                  : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
                    "v"(a[8]), "v"(a[9]));
+  } else if constexpr (N == 16) {
+    asm volatile("ds_read_b128 %0, %16\n ds_read_b128 %1, %17\n ds_read_b128 %2, %18\n ds_read_b128 %3, %19\n"
+                 " ds_read_b128 %4, %20\n ds_read_b128 %5, %21\n ds_read_b128 %6, %22\n ds_read_b128 %7, %23\n"
+                 " ds_read_b128 %8, %24\n ds_read_b128 %9, %25\n ds_read_b128 %10, %26\n ds_read_b128 %11, %27\n"
+                 " ds_read_b128 %12, %28\n ds_read_b128 %13, %29\n ds_read_b128 %14, %30\n ds_read_b128 %15, %31\n"
+                 " s_waitcnt lgkmcnt(0)"
+                 : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]),
+                   "=&v"(f[7]), "=&v"(f[8]), "=&v"(f[9]), "=&v"(f[10]), "=&v"(f[11]), "=&v"(f[12]), "=&v"(f[13]),
+                   "=&v"(f[14]), "=&v"(f[15])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
+                   "v"(a[8]), "v"(a[9]), "v"(a[10]), "v"(a[11]), "v"(a[12]), "v"(a[13]), "v"(a[14]), "v"(a[15]));
   } else {
     asm volatile("ds_read_b128 %0, %12\n ds_read_b128 %1, %13\n ds_read_b128 %2, %14\n ds_read_b128 %3, %15\n"
                  " ds_read_b128 %4, %16\n ds_read_b128 %5, %17\n ds_read_b128 %6, %18\n ds_read_b128 %7, %19\n"
@@ -1713,6 +1724,132 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_w8a16_dma_kernel(
   });
 }
 
+// grouped_gemm_w8a16_dma_kernel's chunk loop (tiles of at most 64 rows) on a ring of three chunk
+// stages: as grouped_gemm_ring_kernel does for bf16, the DMA goes two chunks ahead, the chunk's
+// fragments (both halves: e4m3 weight rows, then the activations of each MFMA step) are read in one
+// asm block that ends waiting for them, the weights are widened after it, and each chunk ends
+// waiting for its wave's next chunk only.  Same MFMAs in the same order: bit-identical.  K % 128 == 0.
+template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
+__global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_w8a16_ring_kernel(GemmArgs p) {
+  using G = Geo<BM, BN, WGM, WGN, EPI>;
+  constexpr int BK = G::BK;
+  constexpr int NW = G::NW;
+  constexpr int A_PW = BM / 8 / NW;
+  constexpr int B_PW = BN / 8 / NW;
+  static_assert(A_PW * 8 * NW == BM && B_PW * 8 * NW == BN, "slab split over waves");
+  static_assert(BM <= 64, "chunk stages");
+  struct Stage {
+    uint16_t a[2 * BM * BK];   // two 64-k activation slabs
+    uint16_t b[BN * BK];       // BN rows of 128 e4m3 bytes
+  };
+  __shared__ __attribute__((aligned(1024))) Stage t0;
+  __shared__ __attribute__((aligned(1024))) Stage t1;
+  __shared__ __attribute__((aligned(1024))) Stage t2;
+  __shared__ int s_pref[kMaxSeg + 1];
+
+  TileCoord tc;
+  if (!decode_tile<BM, G::OUT_BN, GM>(p, s_pref, tc)) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane >> 3;
+  const long long k0 = static_cast<long long>(tc.split) * p.K;
+  const BufRef rA{static_cast<const uint8_t*>(p.a) + k0 * 2, (p.a_rows_cap * p.lda - k0) * 2};
+  uint32_t a_voff[A_PW];
+  a_offsets<A_PW, NW>(p, tc, wave, lane, 2, a_voff);
+  const uint8_t* b_base = expert_weights(p, tc.expert, 1) + k0;
+  const BufRef rB{b_base, p.b_estride - k0};
+  uint32_t b_voff[B_PW];
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i) {
+    const int R = (wave * B_PW + i) * 8 + lrow;
+    const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
+    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb + (((lane & 7) ^ swz(R)) << 4));
+  }
+  const int wm = wave % WGM;
+  const int wn = wave / WGM;
+  const int NC = p.K / 128;   // 128-k chunks
+  const bool nt = p.b_nt != 0 || tc.one_mt != 0;
+  const float* scale = p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows;
+  const int lr = lane & 15;
+  const int q = lane >> 4;
+  by_height<BM, G::MB, A_PW>(tc.row_end - tc.row0, [&]<int MBE>() {
+    constexpr int A_CNT = A_PW * MBE / G::MB;
+    constexpr int L = 2 * A_CNT + B_PW;          // DMA instructions per chunk per wave
+    constexpr int NF = 2 * (G::NB + 2 * MBE);    // fragment reads per chunk
+    f32x4_t acc[MBE][G::NB];
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto issue_chunk = [&](int c, Stage& st) __attribute__((always_inline)) {
+      issue_a_dma<A_CNT, NW>(rA, a_voff, st.a, wave, c * 256);
+      issue_a_dma<A_CNT, NW>(rA, a_voff, st.a + BM * BK, wave, c * 256 + 128);
+      issue_b8_dma<B_PW, NW>(rB, b_voff, st.b, wave, c * 128, nt);
+    };
+    // fragment addresses of a stage: per half h, the NB weight rows, then the MBE activation
+    // fragments of step 0 and of step 1 (the k assignment of w8a16_slab_mma)
+    auto chunk_mma = [&](const Stage& st) __attribute__((always_inline)) {
+      const uint32_t aA = lds_addr(st.a);
+      const uint32_t aB = lds_addr(st.b);
+      uint32_t ad[NF];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        constexpr int PH = G::NB + 2 * MBE;
+#pragma unroll
+        for (int j = 0; j < G::NB; ++j) {
+          const int R = wn * G::WN + j * 16 + lr;
+          ad[h * PH + j] = aB + R * 128 + (((4 * h + q) ^ swz(R)) << 4);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int i = 0; i < MBE; ++i) {
+            const int R = wm * 16 * MBE + i * 16 + lr;
+            ad[h * PH + G::NB + kk * MBE + i] = aA + 2 * (h * BM * BK + R * BK + (((2 * q + kk) ^ swz(R)) << 3));
+          }
+      }
+      bf16x8_t fr[NF];
+      lds_read_wait(ad, fr);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        constexpr int PH = G::NB + 2 * MBE;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          bf16x8_t af[MBE], bw[G::NB];
+#pragma unroll
+          for (int i = 0; i < MBE; ++i) af[i] = fr[h * PH + G::NB + kk * MBE + i];
+#pragma unroll
+          for (int j = 0; j < G::NB; ++j) {
+            const u32x4_t raw = __builtin_bit_cast(u32x4_t, fr[h * PH + j]);
+            bw[j] = widen_fp8x8(raw[2 * kk], raw[2 * kk + 1]);
+          }
+          mma<G, MBE>(acc, af, bw);
+        }
+      }
+    };
+    issue_chunk(0, t0);
+    issue_chunk(min(1, NC - 1), t1);
+    wait_vm<L>();   // this wave's chunk 0
+    pp_barrier();
+#define EIMOE_W8R_CHUNK(J, ST, STN)                  \
+  if (c + J < NC) {                                 \
+    issue_chunk(min(c + J + 2, NC - 1), STN);       \
+    chunk_mma(ST);                                  \
+    wait_vm<L>();                                   \
+    pp_barrier();                                   \
+  }
+    for (int c = 0; c < NC; c += 3) {
+      EIMOE_W8R_CHUNK(0, t0, t2)
+      EIMOE_W8R_CHUNK(1, t1, t0)
+      EIMOE_W8R_CHUNK(2, t2, t1)
+    }
+#undef EIMOE_W8R_CHUNK
+    pp_wait_vm0();   // the clamped loads near the end land before the workgroup's LDS is released
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale, nullptr);   // bf16 activations
+  });
+}
+
 // ---------------------------------------------------------------------------- launch
 // bf16 LDS tiles of at most 64 rows: the three-stage ring (grouped_gemm_ring_kernel) holds two slabs
 // in flight per workgroup instead of one, but at fewer workgroups per CU (LDS: 32x128 3 -> 2,
@@ -1723,18 +1860,20 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_w8a16_dma_kernel(
 // 0.170 / 0.222 -> 0.200 ms cold, Qwen3-30B-A3B share 256 tokens 95 -> 93 us, but the share at 768
 // tokens 90 -> 92 us (its down projection, ~640 tiles of 64x128, one round of the two-stage kernel's
 // 768 slots and 1.25 of the ring's 512).
-static int lds_tile_wgs(int bm, int bn, int stages) {
-  const int bytes = stages * (bm + bn) * 64 * 2 + (kMaxSeg + 1) * 4;
+// Workgroups per CU that a tile's LDS allows: `stages` stages of stage_bytes and the segment prefix.
+static int lds_tile_wgs(int stage_bytes, int stages) {
+  const int bytes = stages * stage_bytes + (kMaxSeg + 1) * 4;
   const int kib = (bytes + 1023) / 1024;
   return 160 / kib;
 }
 
-static bool use_ring_tile(const GemmArgs& p, int bm, int bn, int n_tiles) {
+// stage_bytes: one stage of the tile (bf16: a 64-k slab of A and B; W8A16: a 128-k chunk of both).
+static bool use_ring_tile(const GemmArgs& p, int bm, int stage_bytes, int n_tiles) {
   const int S = p.S > 0 ? p.S : 1;
   const double avg = static_cast<double>(p.rows_hint > 0 ? std::min(p.rows_hint, p.max_rows) : p.max_rows) / S;
   const double est = static_cast<double>(S) * std::ceil(avg / bm) * n_tiles * p.k_split;
-  const double slots2 = static_cast<double>(lds_tile_wgs(bm, bn, 2)) * kNumCu;
-  const double slots3 = static_cast<double>(lds_tile_wgs(bm, bn, 3)) * kNumCu;
+  const double slots2 = static_cast<double>(lds_tile_wgs(stage_bytes, 2)) * kNumCu;
+  const double slots3 = static_cast<double>(lds_tile_wgs(stage_bytes, 3)) * kNumCu;
   return est > slots2 || est * 1.3 <= slots3;
 }
 
@@ -1756,6 +1895,13 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
     // widened through registers on their way to LDS
     if constexpr (BM <= 128) {
       if (p.K % 128 == 0) {
+        if constexpr (BM <= 64) {
+          if (use_ring_tile(p, BM, (2 * BM + BN) * 128, n_tiles)) {
+            hipLaunchKernelGGL((grouped_gemm_w8a16_ring_kernel<BM, BN, WGM, WGN, EPI, GM>),
+                               dim3(static_cast<unsigned>(grid)), dim3(WGM * WGN * 64), 0, s, p);
+            return hipGetLastError();
+          }
+        }
         hipLaunchKernelGGL((grouped_gemm_w8a16_dma_kernel<BM, BN, WGM, WGN, EPI, GM>),
                            dim3(static_cast<unsigned>(grid)), dim3(WGM * WGN * 64), 0, s, p);
         return hipGetLastError();
@@ -1765,7 +1911,7 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
                        dim3(WGM * WGN * 64), 0, s, p);
   } else {
     if constexpr (BM <= 64) {
-      if (use_ring_tile(p, BM, BN, n_tiles)) {
+      if (use_ring_tile(p, BM, (BM + BN) * 128, n_tiles)) {
         hipLaunchKernelGGL((grouped_gemm_ring_kernel<BM, BN, WGM, WGN, EPI, GM, 3>), dim3(static_cast<unsigned>(grid)),
                            dim3(WGM * WGN * 64), 0, s, p);
         return hipGetLastError();

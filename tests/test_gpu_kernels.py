@@ -945,41 +945,48 @@ def test_fp32_gemms_explicit_tile_narrow_columns(dev, tile):
         torch.testing.assert_close(c[a:b], yref, rtol=2e-5, atol=2e-6)
 
 
-# The bf16 LDS tiles of up to 64 rows run on a three-stage ring (grouped_gemm_ring_kernel) unless the
-# two-stage kernel would hold a launch's estimated tiles in one round and the ring would not; with
-# no expected rows given the estimate takes the row bound.  The same segments under two row bounds,
-# one in each regime (the rule restated below), must agree bit for bit: gathered rows, remainder
-# heights, empty segments, K split planes.
-def _lds_tile_wgs(bm, bn, stages):
-    kib = -(-(stages * (bm + bn) * 128 + 1025 * 4) // 1024)
+# The LDS tiles of up to 64 rows (bf16, and W8A16 with e4m3 weights) run on a three-stage ring
+# (grouped_gemm_ring_kernel, grouped_gemm_w8a16_ring_kernel) unless the two-stage kernel would hold a
+# launch's estimated tiles in one round and the ring would not; with no expected rows given the
+# estimate takes the row bound.  The same segments under two row bounds, one in each regime (the rule
+# restated below), must agree bit for bit: gathered rows, remainder heights, empty segments, K split
+# planes.
+def _lds_tile_wgs(stage_bytes, stages):
+    kib = -(-(stages * stage_bytes + 1025 * 4) // 1024)
     return 160 // kib
 
 
-def _ring_taken(bm, bn, S, max_rows, n_tiles, ks):
+def _ring_taken(bm, stage_bytes, S, max_rows, n_tiles, ks):
     est = S * math.ceil(max_rows / S / bm) * n_tiles * ks
-    return est > _lds_tile_wgs(bm, bn, 2) * 256 or est * 1.3 <= _lds_tile_wgs(bm, bn, 3) * 256
+    return est > _lds_tile_wgs(stage_bytes, 2) * 256 or est * 1.3 <= _lds_tile_wgs(stage_bytes, 3) * 256
 
 
-def _two_stage_bound(bm, bn, S, n_tiles, ks):
+def _two_stage_bound(bm, stage_bytes, S, n_tiles, ks):
     for m in range(1, 200):
-        if not _ring_taken(bm, bn, S, S * bm * m, n_tiles, ks):
+        if not _ring_taken(bm, stage_bytes, S, S * bm * m, n_tiles, ks):
             return S * bm * m
     raise AssertionError("no row bound in the two-stage band")
 
 
+@pytest.mark.parametrize("fp8w", [False, True])
 @pytest.mark.parametrize("tile,bm,bn", [(3, 32, 128), (6, 64, 128), (4, 16, 64)])
-def test_ring_lds_tiles_bit_identical_with_two_stage(dev, tile, bm, bn):
+def test_ring_lds_tiles_bit_identical_with_two_stage(dev, tile, bm, bn, fp8w):
     counts = [40, 0, 3, 70, 17, 33, 1, 64]
     S, rows = len(counts), sum(counts)
-    g = torch.Generator().manual_seed(300 + tile)
+    g = torch.Generator().manual_seed(300 + tile + 10 * fp8w)
     H, I, T = 256, 256, 97
     off_t = _segments(counts)[1].to(dev)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
     wgu = (torch.randn(S, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16).to(dev)
     wd = (torch.randn(S, H, I, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    sgu = sd = None
+    if fp8w:
+        wgu, sgu = ops.quantize_weights_fp8(wgu)
+        wd, sd = ops.quantize_weights_fp8(wd)
+    stage = (2 * bm + bn) * 128 if fp8w else (bm + bn) * 128
     nt_gu, nt_dn = I // (bn // 2), H // bn
-    bounds = {"gu": _two_stage_bound(bm, bn, S, nt_gu, 1), "dn1": _two_stage_bound(bm, bn, S, nt_dn, 1),
-              "dn2": _two_stage_bound(bm, bn, S, nt_dn, 2)}
+    bounds = {"gu": _two_stage_bound(bm, stage, S, nt_gu, 1), "dn1": _two_stage_bound(bm, stage, S, nt_dn, 1),
+              "dn2": _two_stage_bound(bm, stage, S, nt_dn, 2)}
     big = max(bounds.values())
     a_rows = torch.zeros(big, dtype=torch.int32)
     a_rows[:rows] = torch.randint(0, T, (rows,), generator=g, dtype=torch.int32)
@@ -987,10 +994,10 @@ def test_ring_lds_tiles_bit_identical_with_two_stage(dev, tile, bm, bn):
     hs = torch.zeros(big, I, dtype=torch.bfloat16)
     hs[:rows] = torch.randn(rows, I, generator=g).to(torch.bfloat16)
     hs = hs.to(dev)
-    assert _ring_taken(bm, bn, S, rows, nt_gu, 1) and _ring_taken(bm, bn, S, rows, nt_dn, 2)
-    gu = lambda mr: cpu(ops.gemm_gate_up_silu(x, wgu, off_t, mr, a_rows=a_rows[:mr], tile=tile))[:rows]
+    assert _ring_taken(bm, stage, S, rows, nt_gu, 1) and _ring_taken(bm, stage, S, rows, nt_dn, 2)
+    gu = lambda mr: cpu(ops.gemm_gate_up_silu(x, wgu, off_t, mr, a_rows=a_rows[:mr], w_scale=sgu, tile=tile))[:rows]
     assert torch.equal(gu(rows), gu(bounds["gu"]))
     for ks in (1, 2):
-        dn = lambda mr: cpu(ops.gemm_down(hs[:mr], wd, off_t, mr, out_dtype=torch.float32, k_split=ks,
+        dn = lambda mr: cpu(ops.gemm_down(hs[:mr], wd, off_t, mr, out_dtype=torch.float32, k_split=ks, w_scale=sd,
                                           tile=tile))[:, :rows]
         assert torch.equal(dn(rows), dn(bounds[f"dn{ks}"]))
