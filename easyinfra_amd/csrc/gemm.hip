@@ -1850,6 +1850,121 @@ __global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_w8a16_ring_kernel
   });
 }
 
+// grouped_gemm_fp8_kernel (W8A8, e4m3 x e4m3) on the three-stage ring of grouped_gemm_ring_kernel:
+// a 128-k slab is a 128-byte row of either operand, a fragment two 16-byte chunks of it (frag_fp8),
+// read in one asm block; each accumulator takes one MFMA per slab, as in slab_mma_fp8, so results
+// are bit-identical.
+template <int BM, int BN, int WGM, int WGN, int EPI, int GM>
+__global__ void __launch_bounds__(WGM * WGN * 64) grouped_gemm_fp8_ring_kernel(GemmArgs p) {
+  using G = Geo<BM, BN, WGM, WGN, EPI>;
+  constexpr int BKB = 128;   // K per slab = bytes per LDS row
+  constexpr int NW = G::NW;
+  constexpr int A_PW = BM / 8 / NW;
+  constexpr int B_PW = BN / 8 / NW;
+  static_assert(A_PW * 8 * NW == BM && B_PW * 8 * NW == BN, "slab split over waves");
+  struct Stage {
+    uint16_t a[BM * 64];   // BM rows of 128 e4m3 bytes (the DMA helpers count in 2-byte units)
+    uint16_t b[BN * 64];
+  };
+  __shared__ __attribute__((aligned(1024))) Stage t0;
+  __shared__ __attribute__((aligned(1024))) Stage t1;
+  __shared__ __attribute__((aligned(1024))) Stage t2;
+  __shared__ int s_pref[kMaxSeg + 1];
+
+  TileCoord tc;
+  if (!decode_tile<BM, G::OUT_BN, GM>(p, s_pref, tc)) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane >> 3;
+  const long long k0 = static_cast<long long>(tc.split) * p.K;
+  const BufRef rA{static_cast<const uint8_t*>(p.a) + k0, p.a_rows_cap * p.lda - k0};
+  uint32_t a_voff[A_PW];
+  a_offsets<A_PW, NW>(p, tc, wave, lane, 1, a_voff);
+  const uint8_t* b_base = expert_weights(p, tc.expert, 1) + k0;
+  const BufRef rB{b_base, p.b_estride - k0};
+  uint32_t b_voff[B_PW];
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i) {
+    const int R = (wave * B_PW + i) * 8 + lrow;
+    const int wr = G::weight_row_of_lds(R, tc.n_tile, p.up_off);
+    b_voff[i] = static_cast<uint32_t>(static_cast<long long>(wr) * p.ldb + (((lane & 7) ^ swz(R)) << 4));
+  }
+  const int wm = wave % WGM;
+  const int wn = wave / WGM;
+  const int KT = p.K / BKB;
+  const bool b_nt = p.b_nt != 0 || tc.one_mt != 0;
+  const float* scale = p.b_scale + static_cast<long long>(tc.expert) * p.nb_rows;
+  const int lr = lane & 15;
+  const int q = lane >> 4;
+  by_height<BM, G::MB, A_PW>(tc.row_end - tc.row0, [&]<int MBE>() {
+    constexpr int A_CNT = A_PW * MBE / G::MB;
+    constexpr int L = A_CNT + B_PW;
+    constexpr int NF = 2 * (MBE + G::NB);   // 16-byte reads per slab
+    f32x4_t acc[MBE][G::NB];
+#pragma unroll
+    for (int i = 0; i < MBE; ++i)
+#pragma unroll
+      for (int j = 0; j < G::NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto slab = [&](const Stage& st) __attribute__((always_inline)) {
+      const uint32_t aA = lds_addr(st.a);
+      const uint32_t aB = lds_addr(st.b);
+      uint32_t ad[NF];
+#pragma unroll
+      for (int i = 0; i < MBE; ++i) {
+        const int R = wm * 16 * MBE + i * 16 + lr;
+        ad[2 * i] = aA + R * 128 + ((q ^ swz(R)) << 4);
+        ad[2 * i + 1] = aA + R * 128 + (((q + 4) ^ swz(R)) << 4);
+      }
+#pragma unroll
+      for (int j = 0; j < G::NB; ++j) {
+        const int R = wn * G::WN + j * 16 + lr;
+        ad[2 * (MBE + j)] = aB + R * 128 + ((q ^ swz(R)) << 4);
+        ad[2 * (MBE + j) + 1] = aB + R * 128 + (((q + 4) ^ swz(R)) << 4);
+      }
+      bf16x8_t fr[NF];
+      lds_read_wait(ad, fr);
+      i32x8_t af[MBE], bf[G::NB];
+#pragma unroll
+      for (int i = 0; i < MBE; ++i) {
+        const u32x4_t lo = __builtin_bit_cast(u32x4_t, fr[2 * i]);
+        const u32x4_t hi = __builtin_bit_cast(u32x4_t, fr[2 * i + 1]);
+        af[i] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int j = 0; j < G::NB; ++j) {
+        const u32x4_t lo = __builtin_bit_cast(u32x4_t, fr[2 * (MBE + j)]);
+        const u32x4_t hi = __builtin_bit_cast(u32x4_t, fr[2 * (MBE + j) + 1]);
+        bf[j] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int i = 0; i < MBE; ++i)
+#pragma unroll
+        for (int j = 0; j < G::NB; ++j) acc[i][j] = mfma_fp8(af[i], bf[j], acc[i][j]);
+    };
+    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, t0.a, t0.b, wave, 0, b_nt);
+    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, t1.a, t1.b, wave, min(1, KT - 1) * BKB, b_nt);
+    wait_vm<L>();   // this wave's slab 0
+    pp_barrier();
+#define EIMOE_F8R_SLAB(J, ST, STN)                                                                 \
+  if (kt + J < KT) {                                                                              \
+    issue_slab_dma<A_CNT, B_PW, NW>(rA, rB, a_voff, b_voff, STN.a, STN.b, wave,                     \
+                                    min(kt + J + 2, KT - 1) * BKB, b_nt);                         \
+    slab(ST);                                                                                     \
+    wait_vm<L>();                                                                                 \
+    pp_barrier();                                                                                 \
+  }
+    for (int kt = 0; kt < KT; kt += 3) {
+      EIMOE_F8R_SLAB(0, t0, t2)
+      EIMOE_F8R_SLAB(1, t1, t0)
+      EIMOE_F8R_SLAB(2, t2, t1)
+    }
+#undef EIMOE_F8R_SLAB
+    pp_wait_vm0();   // the clamped loads near the end land before the workgroup's LDS is released
+    epilogue<G, EPI, MBE>(p, tc, acc, wm, wn, lane, scale, p.a_scale);
+  });
+}
+
 // ---------------------------------------------------------------------------- launch
 // bf16 LDS tiles of at most 64 rows: the three-stage ring (grouped_gemm_ring_kernel) holds two slabs
 // in flight per workgroup instead of one, but at fewer workgroups per CU (LDS: 32x128 3 -> 2,
@@ -1888,6 +2003,13 @@ static hipError_t launch_cfg(const GemmArgs& p, int max_rows, bool a_fp8, hipStr
   if (grid > 0x7fffffffll) return hipErrorInvalidValue;
   // A plain runtime branch: the kernels of a configuration are instantiated together.
   if (BFP8 && a_fp8) {
+    if constexpr (BM <= 64) {
+      if (use_ring_tile(p, BM, (BM + BN) * 128, n_tiles)) {
+        hipLaunchKernelGGL((grouped_gemm_fp8_ring_kernel<BM, BN, WGM, WGN, EPI, GM>),
+                           dim3(static_cast<unsigned>(grid)), dim3(WGM * WGN * 64), 0, s, p);
+        return hipGetLastError();
+      }
+    }
     hipLaunchKernelGGL((grouped_gemm_fp8_kernel<BM, BN, WGM, WGN, EPI, GM>), dim3(static_cast<unsigned>(grid)),
                        dim3(WGM * WGN * 64), 0, s, p);
   } else if (BFP8) {

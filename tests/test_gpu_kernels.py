@@ -945,8 +945,8 @@ def test_fp32_gemms_explicit_tile_narrow_columns(dev, tile):
         torch.testing.assert_close(c[a:b], yref, rtol=2e-5, atol=2e-6)
 
 
-# The LDS tiles of up to 64 rows (bf16, and W8A16 with e4m3 weights) run on a three-stage ring
-# (grouped_gemm_ring_kernel, grouped_gemm_w8a16_ring_kernel) unless the two-stage kernel would hold a
+# The LDS tiles of up to 64 rows (bf16, W8A16 and W8A8) run on a three-stage ring (grouped_gemm_ring_kernel,
+# grouped_gemm_w8a16_ring_kernel, grouped_gemm_fp8_ring_kernel) unless the two-stage kernel would hold a
 # launch's estimated tiles in one round and the ring would not; with no expected rows given the
 # estimate takes the row bound.  The same segments under two row bounds, one in each regime (the rule
 # restated below), must agree bit for bit: gathered rows, remainder heights, empty segments, K split
@@ -968,22 +968,22 @@ def _two_stage_bound(bm, stage_bytes, S, n_tiles, ks):
     raise AssertionError("no row bound in the two-stage band")
 
 
-@pytest.mark.parametrize("fp8w", [False, True])
+@pytest.mark.parametrize("mode", ["bf16", "w8a16", "w8a8"])
 @pytest.mark.parametrize("tile,bm,bn", [(3, 32, 128), (6, 64, 128), (4, 16, 64)])
-def test_ring_lds_tiles_bit_identical_with_two_stage(dev, tile, bm, bn, fp8w):
+def test_ring_lds_tiles_bit_identical_with_two_stage(dev, tile, bm, bn, mode):
     counts = [40, 0, 3, 70, 17, 33, 1, 64]
     S, rows = len(counts), sum(counts)
-    g = torch.Generator().manual_seed(300 + tile + 10 * fp8w)
+    g = torch.Generator().manual_seed(300 + tile + 10 * len(mode))
     H, I, T = 256, 256, 97
     off_t = _segments(counts)[1].to(dev)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
     wgu = (torch.randn(S, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16).to(dev)
     wd = (torch.randn(S, H, I, generator=g) * 0.05).to(torch.bfloat16).to(dev)
     sgu = sd = None
-    if fp8w:
+    if mode != "bf16":
         wgu, sgu = ops.quantize_weights_fp8(wgu)
         wd, sd = ops.quantize_weights_fp8(wd)
-    stage = (2 * bm + bn) * 128 if fp8w else (bm + bn) * 128
+    stage = (2 * bm + bn) * 128 if mode == "w8a16" else (bm + bn) * 128
     nt_gu, nt_dn = I // (bn // 2), H // bn
     bounds = {"gu": _two_stage_bound(bm, stage, S, nt_gu, 1), "dn1": _two_stage_bound(bm, stage, S, nt_dn, 1),
               "dn2": _two_stage_bound(bm, stage, S, nt_dn, 2)}
@@ -995,9 +995,18 @@ def test_ring_lds_tiles_bit_identical_with_two_stage(dev, tile, bm, bn, fp8w):
     hs[:rows] = torch.randn(rows, I, generator=g).to(torch.bfloat16)
     hs = hs.to(dev)
     assert _ring_taken(bm, stage, S, rows, nt_gu, 1) and _ring_taken(bm, stage, S, rows, nt_dn, 2)
-    gu = lambda mr: cpu(ops.gemm_gate_up_silu(x, wgu, off_t, mr, a_rows=a_rows[:mr], w_scale=sgu, tile=tile))[:rows]
+    if mode == "w8a8":
+        xq, sx = ops.quantize_rows_fp8(x)
+        hq, sh = ops.quantize_rows_fp8(hs)
+        gu = lambda mr: cpu(ops.gemm_gate_up_silu_w8a8(xq, sx, wgu, sgu, off_t, mr, a_rows=a_rows[:mr],
+                                                       tile=tile))[:rows]
+        dn = lambda mr, ks: cpu(ops.gemm_down_w8a8(hq[:mr], sh[:mr], wd, sd, off_t, mr, k_split=ks,
+                                                   tile=tile))[:, :rows]
+    else:
+        gu = lambda mr: cpu(ops.gemm_gate_up_silu(x, wgu, off_t, mr, a_rows=a_rows[:mr], w_scale=sgu,
+                                                  tile=tile))[:rows]
+        dn = lambda mr, ks: cpu(ops.gemm_down(hs[:mr], wd, off_t, mr, out_dtype=torch.float32, k_split=ks,
+                                              w_scale=sd, tile=tile))[:, :rows]
     assert torch.equal(gu(rows), gu(bounds["gu"]))
     for ks in (1, 2):
-        dn = lambda mr: cpu(ops.gemm_down(hs[:mr], wd, off_t, mr, out_dtype=torch.float32, k_split=ks, w_scale=sd,
-                                          tile=tile))[:, :rows]
-        assert torch.equal(dn(rows), dn(bounds[f"dn{ks}"]))
+        assert torch.equal(dn(rows, ks), dn(bounds[f"dn{ks}"], ks))
