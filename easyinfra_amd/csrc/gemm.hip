@@ -2176,15 +2176,20 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
   if (expert_bytes >= 32.0 * 1024 * 1024) {
     // (W8A8 gate/up at 16 rows per expert on the routed, gathered rows of a Mixtral-8x7B
     // decode batch: 182 us on 32x128 tiles, 190 us streamed.  bf16 down projection on 128x128
-    // with its K split 2 from 4 expected rows, streaming below: Mixtral-8x7B layers at 16 / 20 /
+    // with its K split 2, first from 4 expected rows: Mixtral-8x7B layers at 16 / 20 /
     // 24 / 28 tokens 488 / 499 / 492 / 499 -> 459 / 456 / 462 / 458 us cold, where streaming with a
     // K split of 8 had run to 8 rows; 12 and 32 tokens unchanged.  bf16 gate/up on 256x256 from 64
     // rows: layers at 256 / 320 / 384 / 448 tokens 524 / 543 / 555 / 578 -> 511 / 516 / 544 / 552 us
     // cold against 128x128 up to 128 rows; 192 tokens unchanged.  W8A8 likewise on 256x256 from 64
     // rows: 256 / 320 / 384 / 448 tokens 323 / 340 / 355 / 368 -> 316 / 316 / 334 / 342 us)
     if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 64 ? kTileM : kTileL;
-    else if (silu) t = avg < 24 ? kTileXS : avg < 64 ? kTileM : kTileL;
-    else t = avg < 4 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    // bf16 from one expected row per expert: the gate/up on 32x128 tiles (the three-stage ring) to
+    // 24 rows, the down projection on 128x128 (Mixtral-8x7B layers, cold, one box, at 4 / 8 / 12 / 16
+    // / 32 / 64 / 96 tokens 332 / 395 / 458 / 460 / 460 / 468 / 464 -> 318 / 353 / 394 / 419 / 421 /
+    // 427 / 435 us against streaming both below 24 / 4 rows; at 128 tokens, 32 rows, half the
+    // experts take a second 32-row m-tile whose weight panel comes again from HBM: 482 -> 650 us)
+    else if (silu) t = avg < 1 ? kTileXS : avg < 25 ? kTileS : avg < 64 ? kTileM : kTileL;
+    else t = avg < 1 ? kTileXS : avg < 128 ? kTileM : kTileL;
   } else if (silu) {
     // From the row bound, not the expected rows: the Qwen3-30B-A3B 32-expert share at 2048
     // tokens (~3900 local rows, 56-551 per expert) measured 72 us on 256x256 tiles and 89 us on
