@@ -2182,7 +2182,9 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
     // rows: layers at 256 / 320 / 384 / 448 tokens 524 / 543 / 555 / 578 -> 511 / 516 / 544 / 552 us
     // cold against 128x128 up to 128 rows; 192 tokens unchanged.  W8A8 likewise on 256x256 from 64
     // rows: 256 / 320 / 384 / 448 tokens 323 / 340 / 355 / 368 -> 316 / 316 / 334 / 342 us)
-    if (b_fp8) t = avg < 8 ? kTileXS : avg < 24 ? kTileS : avg < 64 ? kTileM : kTileL;
+    // (W8A8 on 32x128, the three-stage ring, to 24 rows included: 96 tokens 262 -> 244 us cold against
+    // 128x128; 16x64 rather than 32x128 below 8 rows, equal on the ring at 4-32 tokens)
+    if (b_fp8) t = avg < 8 ? kTileXS : avg < 25 ? kTileS : avg < 64 ? kTileM : kTileL;
     // bf16 from one expected row per expert: the gate/up on 32x128 tiles (the three-stage ring) to
     // 24 rows, the down projection on 128x128 (Mixtral-8x7B layers, cold, one box, at 4 / 8 / 12 / 16
     // / 32 / 64 / 96 tokens 332 / 395 / 458 / 460 / 460 / 468 / 464 -> 318 / 353 / 394 / 419 / 421 /
