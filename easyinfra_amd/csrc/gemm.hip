@@ -2183,8 +2183,10 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
     // cold against 128x128 up to 128 rows; 192 tokens unchanged.  W8A8 likewise on 256x256 from 64
     // rows: 256 / 320 / 384 / 448 tokens 323 / 340 / 355 / 368 -> 316 / 316 / 334 / 342 us)
     // (W8A8 on 32x128, the three-stage ring, to 24 rows included: 96 tokens 262 -> 244 us cold against
-    // 128x128; 16x64 rather than 32x128 below 8 rows, equal on the ring at 4-32 tokens)
-    if (b_fp8) t = avg < 8 ? kTileXS : avg < 25 ? kTileS : avg < 64 ? kTileM : kTileL;
+    // 128x128; 16x64 rather than 32x128 below 8 rows, equal on the ring at 4-32 tokens; 64x128, the
+    // ring, to 56 rows: 104 / 128 / 160 / 192 / 224 tokens 265 / 273 / 282 / 293 / 301 -> 246 / 253 /
+    // 262 / 272 / 281 us against 128x128, but 240 tokens, 60 rows, 313 -> 334)
+    if (b_fp8) t = avg < 8 ? kTileXS : avg < 25 ? kTileS : avg < 58 ? kTileMS : avg < 64 ? kTileM : kTileL;
     // bf16 from one expected row per expert: the gate/up on 32x128 tiles (the three-stage ring) to
     // 24 rows, the down projection on 128x128 (Mixtral-8x7B layers, cold, one box, at 4 / 8 / 12 / 16
     // / 32 / 64 / 96 tokens 332 / 395 / 458 / 460 / 460 / 468 / 464 -> 318 / 353 / 394 / 419 / 421 /
