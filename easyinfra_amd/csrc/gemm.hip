@@ -2187,15 +2187,16 @@ int gemm_pick_tile(const GemmArgs& p, int epi, bool b_fp8) {
     // ring, to 56 rows: 104 / 128 / 160 / 192 / 224 tokens 265 / 273 / 282 / 293 / 301 -> 246 / 253 /
     // 262 / 272 / 281 us against 128x128, but 240 tokens, 60 rows, 313 -> 334)
     if (b_fp8) t = avg < 8 ? kTileXS : avg < 25 ? kTileS : avg < 58 ? kTileMS : avg < 64 ? kTileM : kTileL;
-    // bf16 from one expected row per expert: the gate/up on 32x128 tiles (the three-stage ring) to
+    // bf16 from 0.7 expected rows per expert (3 Mixtral-8x7B tokens 334 -> 318 us; 2 tokens, half a
+    // row, 204 -> 229 on the tiles): the gate/up on 32x128 tiles (the three-stage ring) to
     // 24 rows, the down projection on 128x128 (Mixtral-8x7B layers, cold, one box, at 4 / 8 / 12 / 16
     // / 32 / 64 / 96 tokens 332 / 395 / 458 / 460 / 460 / 468 / 464 -> 318 / 353 / 394 / 419 / 421 /
     // 427 / 435 us against streaming both below 24 / 4 rows; at 128 tokens, 32 rows, half the
     // experts take a second 32-row m-tile whose weight panel comes again from HBM: 482 -> 650 us),
     // then on 64x128 tiles (the ring) to 64 rows (104 / 128 / 160 / 192 / 224 / 240 tokens 470 / 480 /
     // 491 / 503 / 515 / 525 -> 438 / 449 / 457 / 469 / 480 / 517 us against 128x128)
-    else if (silu) t = avg < 1 ? kTileXS : avg < 25 ? kTileS : avg < 64 ? kTileMS : kTileL;
-    else t = avg < 1 ? kTileXS : avg < 128 ? kTileM : kTileL;
+    else if (silu) t = avg < 0.7 ? kTileXS : avg < 25 ? kTileS : avg < 64 ? kTileMS : kTileL;
+    else t = avg < 0.7 ? kTileXS : avg < 128 ? kTileM : kTileL;
   } else if (silu) {
     // From the row bound, not the expected rows: the Qwen3-30B-A3B 32-expert share at 2048
     // tokens (~3900 local rows, 56-551 per expert) measured 72 us on 256x256 tiles and 89 us on
