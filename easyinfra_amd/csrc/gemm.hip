@@ -2155,11 +2155,10 @@ static int routed_small_down_tile(const GemmArgs& p, int S, double avg, int t, b
 // Tile heuristic (the host knows only the row bound, or a caller's estimate, and the shapes).
 // Measured on the routed offsets of the workloads (cold caches; us, gate/up + down):
 //  * experts of >= 32 MiB of weights (Mixtral-8x7B) are read from HBM once per row chunk of
-//    a segment, so the tile should cover a segment in one chunk.  64 tokens (16 rows per
-//    expert): bf16 gate/up streams (335 vs 372 with 32x128), the down projection takes
-//    128x128 with K split 2 (159 vs 178 streaming); e4m3 W8A8 takes 32x128 for both (180
-//    vs 190, 84 vs 97).  128-256 tokens (32-64 rows): 128x128 (gate/up 377 and 402 vs 478
-//    and 911 with 32x128).  From 128 rows: 256x256;
+//    a segment, so the tile should cover a segment in one chunk: the 32x128 and 64x128 tiles
+//    (on the three-stage ring) while the expected rows fit one 32- or 64-row chunk with room
+//    for the spread, the bf16 down projection on 128x128 with K split 2, 256x256 from 64 rows
+//    (the figures beside each rule below);
 //  * small experts (DeepSeek-V2-Lite, Qwen3 local share) stay in cache: gate/up keeps the
 //    256x256 tile from ~256 rows per segment of the bound (DeepSeek 4096 tokens 717 vs 710
 //    us skewed, 580 vs 657 uniform against 128x128); the down projection (short K) wants
